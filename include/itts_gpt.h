@@ -1,0 +1,160 @@
+/* itts_gpt.h — C ABI of the MI355X-native IndexTTS 2.5 GPT semantic-token loop.
+ *
+ * The reference has no FFI: its callers link the C++ class itts25::GptDecoder
+ * (include/itts25/gpt.hpp:19-43).  This header is the boundary that class is
+ * rebuilt on; index-tts-25-metal_amd/cpp/itts25/gpt.hpp keeps the reference's C++
+ * signatures on top of it, and the Python binding (index-tts-25-metal_amd/itts_gpt.py)
+ * binds it with ctypes.  Plain pointers and sizes only; all pointers are host
+ * pointers unless a name says otherwise.
+ *
+ * Status codes mirror the reference's exception kinds:
+ *   ITTS_OK 0, ITTS_EINVAL -1 (std::invalid_argument), ITTS_ERUNTIME -2
+ *   (std::runtime_error), ITTS_ELOGIC -3 (std::logic_error).  The message of the
+ *   last failure on a handle is returned by itts_gpt_last_error(handle); failures
+ *   of itts_gpt_create are reported by itts_gpt_last_error(NULL) (thread local).
+ *
+ * Threading: one handle = one HIP stream; a handle is not reentrant (as the
+ * reference decoder is not, gpt.hpp:22).  Distinct handles may be used from
+ * distinct threads.
+ */
+#ifndef ITTS_GPT_H
+#define ITTS_GPT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ITTS_OK 0
+#define ITTS_EINVAL (-1)
+#define ITTS_ERUNTIME (-2)
+#define ITTS_ELOGIC (-3)
+
+#define ITTS_MEL_VOCAB 8194u
+#define ITTS_MEL_START 8192u
+#define ITTS_MEL_STOP 8193u
+#define ITTS_MAX_BATCH 10u
+
+/* One named host tensor, in the reference bundle's names and HF layouts
+ * (Conv1D weights [in, out]; mel_head and spk_emb_proj [out, in]).
+ * Replaces itts25::Weights::get/info (include/itts25/weights.hpp:9-10). */
+typedef struct {
+    const char* name;
+    const float* data;
+    int64_t shape[4];
+    int32_t ndim;
+    int32_t _pad;
+} itts_tensor;
+
+#define ITTS_WEIGHTS_F32 0u
+#define ITTS_WEIGHTS_BF16 1u
+
+typedef struct {
+    uint32_t kv_capacity;  /* KV rows per sequence; 0 -> 4096 (gpt.cpp:7)            */
+    uint32_t max_batch;    /* sequences for generate_batch / beams; 0 -> 1, <= 10     */
+    uint32_t weight_dtype; /* ITTS_WEIGHTS_F32 or ITTS_WEIGHTS_BF16 (fp32 accumulate) */
+    uint32_t flags;        /* reserved, 0                                             */
+} itts_gpt_config;
+
+/* Field meaning of itts25::GenerationOptions (include/itts25/gpt.hpp:7-16), plus
+ * suppress_stop: when non-zero, raw logits 8192 and 8193 are set to -inf before
+ * any processor so a fixed number of codes is produced (benchmarks; default 0;
+ * no reference counterpart). */
+typedef struct {
+    int32_t do_sample;
+    uint32_t _pad0;
+    uint64_t seed;
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float repetition_penalty;
+    uint32_t num_beams;
+    float length_penalty;
+    uint32_t suppress_stop;
+    uint32_t _pad1;
+} itts_gen_options;
+
+/* Defaults of itts25::GenerationOptions (gpt.hpp:7-16). */
+void itts_gen_options_default(itts_gen_options* o);
+
+typedef struct itts_gpt itts_gpt;
+typedef struct itts_gpt_state itts_gpt_state;
+
+/* GptDecoder::GptDecoder (gpt.cpp:8-23): checks shapes, uploads weights (Conv1D
+ * weights transposed to [out, in] on the device), allocates the KV cache. */
+int itts_gpt_create(const itts_tensor* tensors, int32_t count, const itts_gpt_config* cfg, itts_gpt** out);
+void itts_gpt_destroy(itts_gpt* h);
+const char* itts_gpt_last_error(const itts_gpt* h);
+
+/* GptDecoder::prepare (gpt.cpp:42-71): speaker[192], emotion[1280]; writes the
+ * prefix (rows x 1280) into prefix_out, which holds capacity_rows rows. */
+int itts_gpt_prepare(itts_gpt* h, const float* speaker, const float* emotion, const uint32_t* text, uint32_t n_text,
+                     uint32_t language, float* prefix_out, uint32_t capacity_rows, uint32_t* rows);
+/* Same prefix with caller-given conditioning rows in place of the reference's
+ * [spk_proj(speaker) + emotion, 0, 0] block (gpt.cpp:53-56). */
+int itts_gpt_prepare_cond(itts_gpt* h, const float* cond, uint32_t n_cond, const uint32_t* text, uint32_t n_text,
+                          uint32_t language, float* prefix_out, uint32_t capacity_rows, uint32_t* rows);
+
+/* GptDecoder::prefill (gpt.cpp:72-78): logits[8194] of the last prefix row. */
+int itts_gpt_prefill(itts_gpt* h, const float* prefix, uint32_t rows, float* logits);
+/* GptDecoder::step (gpt.cpp:79-85). */
+int itts_gpt_step(itts_gpt* h, uint32_t code, uint32_t position, float* logits);
+/* GptDecoder::cached_tokens (gpt.hpp:31). */
+uint32_t itts_gpt_cached_tokens(const itts_gpt* h);
+
+/* GptDecoder::checkpoint / restore (gpt.cpp:86-87): a device copy of the cached
+ * KV rows.  A state is released with itts_gpt_state_release. */
+int itts_gpt_checkpoint(itts_gpt* h, itts_gpt_state** out);
+int itts_gpt_restore(itts_gpt* h, const itts_gpt_state* state);
+uint32_t itts_gpt_state_tokens(const itts_gpt_state* state);
+void itts_gpt_state_release(itts_gpt_state* state);
+
+/* GptDecoder::generate (gpt_sampling.cpp:168-245): codes_out holds max_tokens. */
+int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options,
+                      uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped);
+
+/* Independent requests decoded together (no reference counterpart: the reference
+ * runs one request at a time, http.cpp:57).  Sequence b's prefix is prefixes[b]
+ * (rows[b] x 1280); each follows generate()'s semantics with options[b].
+ * codes_out is [batch][max_tokens]. */
+int itts_gpt_generate_batch(itts_gpt* h, uint32_t batch, const float* const* prefixes, const uint32_t* rows,
+                            const itts_gen_options* options, uint32_t max_tokens, uint32_t* codes_out,
+                            uint32_t* n_codes, int32_t* stopped);
+
+/* apply_gpt_sampling_processors (gpt_sampling.cpp:28-128), run on the device. */
+int itts_gpt_apply_processors(itts_gpt* h, const float* logits, uint32_t vocab, const uint32_t* history,
+                              uint32_t n_history, const itts_gen_options* options, float* out);
+/* sample_gpt_token_from_logits (gpt_sampling.cpp:130-165), run on the device with
+ * the SplitMix64 state *rng_state (advanced in place), `draws` times. */
+int itts_gpt_sample(itts_gpt* h, const float* processed, uint32_t vocab, uint64_t* rng_state, uint32_t draws,
+                    uint32_t* tokens);
+
+/* Timing of the last prefill / generate call on the handle's stream, from HIP
+ * events (milliseconds). */
+typedef struct {
+    float prefill_ms;
+    float decode_ms;
+    uint32_t decode_steps;
+    uint32_t _pad;
+} itts_gpt_timing;
+int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
+
+/* Measurement hook (no reference counterpart): launches one decode kernel kind
+ * `iters` times back to back on the handle's stream, layer i % layers for launch i, and
+ * returns the mean launch duration from HIP events and the algorithmic bytes moved per
+ * launch.  which: 0 c_attn GEMV (+LayerNorm, K/V append), 1 attn.c_proj GEMV (+residual),
+ * 2 mlp.c_fc GEMV (+LayerNorm, GELU), 3 mlp.c_proj GEMV (+residual), 4 mel_head GEMV
+ * (+ln_f, final_norm), 5 decode attention at 753 cached rows. */
+int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t iters, float* avg_ms, double* bytes_per_launch);
+
+/* Deterministic N(mean, std^2) fill for synthetic weights and inputs: value i is
+ * a Box-Muller transform of two SplitMix64 outputs keyed by (seed, i), so the
+ * result does not depend on thread count.  Host only. */
+void itts_synthetic_normal(float* out, size_t n, uint64_t seed, float mean, float stddev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

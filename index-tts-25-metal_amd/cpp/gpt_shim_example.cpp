@@ -1,0 +1,89 @@
+// Example caller of the drop-in itts25::GptDecoder, written the way the reference's
+// pipeline holds it (src/pipeline.cpp:12, 23-25): a Weights object with info()/get(),
+// a device-context object, prepare -> generate.  Weights here are a synthetic 2-layer
+// table; `gpt_shim_example run` executes on the GPU, without arguments it only checks
+// that the shim links.
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "itts25/gpt.hpp"
+
+namespace {
+struct TensorInfo {
+    std::vector<int64_t> shape;
+};
+struct TableWeights {  // the reference Weights interface (include/itts25/weights.hpp:9-10)
+    std::map<std::string, TensorInfo> infos;
+    std::map<std::string, std::vector<float>> data;
+    const TensorInfo& info(const std::string& n) const { return infos.at(n); }
+    const std::vector<float>& get(const std::string& n) { return data.at(n); }
+    void add(const std::string& n, std::vector<int64_t> shape, float mean, float sd, uint64_t seed) {
+        size_t count = 1;
+        for (auto s : shape) count *= static_cast<size_t>(s);
+        std::vector<float> v(count);
+        itts_synthetic_normal(v.data(), count, seed, mean, sd);
+        infos[n] = {shape};
+        data[n] = std::move(v);
+    }
+};
+struct DeviceContext {};
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc < 2 || std::strcmp(argv[1], "run") != 0) {
+        std::printf("gpt shim linked\n");
+        return 0;
+    }
+    TableWeights w;
+    uint64_t seed = 1;
+    w.add("gpt.spk_emb_proj.weight", {1280, 192}, 0, 0.02f, seed++);
+    w.add("gpt.spk_emb_proj.bias", {1280}, 0, 0.02f, seed++);
+    w.add("gpt.text_embedding.weight", {12000, 1280}, 0, 0.02f, seed++);
+    w.add("gpt.text_pos_embedding.emb.weight", {602, 1280}, 0, 0.02f, seed++);
+    w.add("gpt.lang_embedding.weight", {107, 1280}, 0, 0.02f, seed++);
+    w.add("gpt.mel_embedding.weight", {8194, 1280}, 0, 0.02f, seed++);
+    w.add("gpt.mel_pos_embedding.emb.weight", {1815, 1280}, 0, 0.02f, seed++);
+    for (const char* n : {"gpt.gpt.ln_f", "gpt.final_norm"}) {
+        w.add(std::string(n) + ".weight", {1280}, 1, 0, seed++);
+        w.add(std::string(n) + ".bias", {1280}, 0, 0, seed++);
+    }
+    w.add("gpt.mel_head.weight", {8194, 1280}, 0, 0.02f, seed++);
+    w.add("gpt.mel_head.bias", {8194}, 0, 0.02f, seed++);
+    for (int i = 0; i < 24; ++i) {
+        const std::string p = "gpt.gpt.h." + std::to_string(i);
+        w.add(p + ".ln_1.weight", {1280}, 1, 0, seed++);
+        w.add(p + ".ln_1.bias", {1280}, 0, 0, seed++);
+        w.add(p + ".attn.c_attn.weight", {1280, 3840}, 0, 0.02f, seed++);
+        w.add(p + ".attn.c_attn.bias", {3840}, 0, 0.02f, seed++);
+        w.add(p + ".attn.c_proj.weight", {1280, 1280}, 0, 0.02f, seed++);
+        w.add(p + ".attn.c_proj.bias", {1280}, 0, 0.02f, seed++);
+        w.add(p + ".ln_2.weight", {1280}, 1, 0, seed++);
+        w.add(p + ".ln_2.bias", {1280}, 0, 0, seed++);
+        w.add(p + ".mlp.c_fc.weight", {1280, 5120}, 0, 0.02f, seed++);
+        w.add(p + ".mlp.c_fc.bias", {5120}, 0, 0.02f, seed++);
+        w.add(p + ".mlp.c_proj.weight", {5120, 1280}, 0, 0.02f, seed++);
+        w.add(p + ".mlp.c_proj.bias", {1280}, 0, 0.02f, seed++);
+    }
+    DeviceContext ctx;
+    itts25::GptDecoder gpt(w, ctx);
+    std::vector<float> speaker(192, 0.1f), emotion(1280, 0.05f);
+    auto prefix = gpt.prepare(speaker, emotion, {5, 17, 300, 1, 0, 42}, 3);
+    itts25::GenerationOptions opt;
+    opt.do_sample = false;
+    opt.repetition_penalty = 1;
+    auto r = gpt.generate(prefix, opt, 8);
+    std::printf("{\"rows\":%zu,\"codes\":%zu,\"stopped\":%d,\"cached\":%u}\n", prefix.size() / 1280, r.codes.size(),
+                r.stopped ? 1 : 0, gpt.cached_tokens());
+    try {
+        gpt.step(9000, 2);
+        return 1;
+    } catch (const std::invalid_argument&) {
+    }
+    auto scores = itts25::apply_gpt_sampling_processors(std::vector<float>(8194, 0.5f), {1, 8192}, itts25::GenerationOptions{});
+    std::printf("{\"processed\":%zu}\n", scores.size());
+    return 0;
+}

@@ -1,0 +1,318 @@
+// Decode-step kernels: LayerNorm-fused FP32/BF16 GEMV family and split-KV decode
+// attention, for 1..10 sequences per launch.
+//
+// GEMV (replaces mit2_linear_gemv_f32, kernels.metal:1054-1080, plus the separate
+// layernorm / gelu / add / kv-store / build-current dispatches of gpt.cpp:99-118):
+//   * weights row-major [out][in]; each 64-lane wave owns RPW whole rows and streams
+//     them with 128-bit (fp32) or 64-bit (bf16) non-temporal loads, all issued before
+//     the prologue so the LayerNorm overlaps the weight fetch;
+//   * lane l multiplies the 16-byte chunks l, l+64, ... of a row with the matching x
+//     chunks, one FMA chain per (row, sequence), then a fixed xor-butterfly wave sum:
+//     no atomics, so results are deterministic and identical for every batch size;
+//   * the prologue computes LayerNorm(s) of the input row per workgroup (the row is
+//     5 KB, cheaper to recompute than to synchronise on); the epilogue adds the bias
+//     after the reduction (kernels.metal:1077-1078) and fuses the GELU, the residual
+//     add, the q write and the in-place K/V append at cache row n.
+// Attention (replaces mit2_gpt_cached_attention_resident_f32, kernels.metal:2064-2145):
+//   * grid (splits, 20 heads, batch); a workgroup takes <= 128 consecutive cache rows
+//     of one head, 16 lanes per row (one float4 of the 64-dim row each), loads all K
+//     and V float4s up front, forms scores (q.k)*rsqrt(64), a max-subtracted exp and a
+//     partial sum of weights and weighted V;
+//   * the last workgroup of a head (atomic ticket) merges the splits with the usual
+//     rescaling exp(m_s - M) and writes out = sum(w v) / sum(w), then re-arms the ticket.
+#include "kernels.h"
+
+namespace itts {
+namespace {
+
+constexpr int kNW = 4;  // waves per GEMV workgroup
+
+template <int COLS, int RPW, int B, typename WT, int PRO, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    constexpr int J = COLS / 256;  // 16-byte chunks per lane per row
+    constexpr int PER = kWidth / 256;
+    static_assert(PRO == kProNone || COLS == kWidth, "LayerNorm prologue is 1280 wide");
+    using LD = WLoad<WT>;
+    using VT = typename LD::vec;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = (blockIdx.x * kNW + wave) * RPW;
+
+    bool any = false;
+    for (int b = 0; b < a.nseq; ++b) any |= a.state[b].active != 0;
+    if (!any) return;
+
+    // Prologue input first, so waiting on it does not wait on the weight stream.
+    float hv[B][PER];
+    if constexpr (PRO == kProLn || PRO == kProLn2) {
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int i = 0; i < PER; ++i) hv[b][i] = a.x[b * a.x_stride + tid + 256 * i];
+    } else if constexpr (PRO == kProEmbedLn) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const bool live = b < a.nseq;
+            const uint32_t tok = live ? a.state[b].token : 0u, pos = live ? a.state[b].position : 0u;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int c = tid + 256 * i;
+                hv[b][i] = a.mel_emb[static_cast<size_t>(tok) * kWidth + c] + a.mel_pos[static_cast<size_t>(pos) * kWidth + c];
+            }
+        }
+    }
+
+    const WT* __restrict__ w = static_cast<const WT*>(a.w);
+    VT wv[RPW][J];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row0 + r;
+        const int rr = row < a.rows ? row : a.rows - 1;  // clamp: loads stay in bounds, result discarded
+#pragma unroll
+        for (int j = 0; j < J; ++j) wv[r][j] = LD::load(w, static_cast<size_t>(rr) * (COLS / 4) + j * 64 + lane);
+    }
+
+    __shared__ float xs[PRO == kProNone ? 4 : B * kWidth];
+    __shared__ float red[B * kNW];
+    if constexpr (PRO != kProNone) {
+        if constexpr (PRO == kProEmbedLn) {
+            if (blockIdx.x == 0) {
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+#pragma unroll
+                    for (int i = 0; i < PER; ++i) a.h_out[b * kWidth + tid + 256 * i] = hv[b][i];
+            }
+        }
+        ln_block<B, PER>(hv, a.ln_w, a.ln_b, red);
+        if constexpr (PRO == kProLn2) ln_block<B, PER>(hv, a.ln2_w, a.ln2_b, red);
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int i = 0; i < PER; ++i) xs[b * kWidth + tid + 256 * i] = hv[b][i];
+        __syncthreads();
+    }
+
+    float acc[RPW][B];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        float4 xv[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            if constexpr (PRO == kProNone)
+                xv[b] = *reinterpret_cast<const float4*>(a.x + b * a.x_stride + (j * 64 + lane) * 4);
+            else
+                xv[b] = *reinterpret_cast<const float4*>(xs + b * kWidth + (j * 64 + lane) * 4);
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const float4 w4 = LD::to_f4(wv[r][j]);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                acc[r][b] = __builtin_fmaf(w4.x, xv[b].x, acc[r][b]);
+                acc[r][b] = __builtin_fmaf(w4.y, xv[b].y, acc[r][b]);
+                acc[r][b] = __builtin_fmaf(w4.z, xv[b].z, acc[r][b]);
+                acc[r][b] = __builtin_fmaf(w4.w, xv[b].w, acc[r][b]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[r][b] = wave_sum(acc[r][b]);
+
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row0 + r;
+        if (row >= a.rows) continue;
+        const float bias = a.bias[row];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            if (lane != ((r * B + b) & 63)) continue;
+            const float v = acc[r][b] + bias;
+            if constexpr (EPI == kEpiQkv) {
+                if (row < kWidth) {
+                    a.q[b * kWidth + row] = v;
+                } else if (b < a.nseq && a.state[b].active) {
+                    const int rr = row - kWidth;
+                    const bool is_v = rr >= kWidth;
+                    const int c = is_v ? rr - kWidth : rr;
+                    const size_t off = static_cast<size_t>(b) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
+                                       (static_cast<size_t>(c >> 6) * a.kv_cap + a.state[b].n) * kHeadDim + (c & 63);
+                    a.kv[off] = v;
+                }
+            } else if constexpr (EPI == kEpiResid) {
+                a.out[b * a.out_stride + row] = a.resid[b * a.out_stride + row] + v;
+            } else if constexpr (EPI == kEpiGelu) {
+                a.out[b * a.out_stride + row] = gelu_f(v);
+            } else {
+                a.out[b * a.out_stride + row] = v;
+            }
+        }
+    }
+}
+
+template <int COLS, int RPW, int PRO, int EPI, int B>
+hipError_t launch_b(const GemvArgs& a, bool bf16, hipStream_t s) {
+    const int rows_per_wg = kNW * RPW;
+    const dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
+    if (bf16)
+        hipLaunchKernelGGL((gemv_kernel<COLS, RPW, B, uint16_t, PRO, EPI>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemv_kernel<COLS, RPW, B, float, PRO, EPI>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int COLS, int RPW, int PRO, int EPI>
+hipError_t launch_gemv(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    switch (gemv_batch_bucket(batch)) {
+        case 1: return launch_b<COLS, RPW, PRO, EPI, 1>(a, bf16, s);
+        case 2: return launch_b<COLS, RPW, PRO, EPI, 2>(a, bf16, s);
+        case 3: return launch_b<COLS, RPW, PRO, EPI, 3>(a, bf16, s);
+        case 4: return launch_b<COLS, RPW, PRO, EPI, 4>(a, bf16, s);
+        case 8: return launch_b<COLS, RPW, PRO, EPI, 8>(a, bf16, s);
+        case 10: return launch_b<COLS, RPW, PRO, EPI, 10>(a, bf16, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ------------------------------------------------------------------ attention
+
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    if (b >= a.nseq) return;
+    const SeqState& st = a.state[b];
+    if (!st.active) return;
+    const int S = a.splits;
+    const int L = static_cast<int>(st.n) + 1;  // cached rows + the row appended by this step
+    const int chunk = (L + S - 1) / S;
+    const int p0 = s * chunk;
+    const int p1 = min(L, p0 + chunk);
+    const int t = threadIdx.x, g = t >> 4, sub = t & 15, lane = t & 63, wave = t >> 6;
+    const float4 q4 = *reinterpret_cast<const float4*>(a.q + b * kWidth + h * kHeadDim + sub * 4);
+
+    constexpr int PER = kAttnMaxChunk / 16;
+    float4 k4[PER], v4[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int p = p0 + g + 16 * i;
+        if (p < p1) {
+            const uint32_t slot = a.table ? a.table[static_cast<size_t>(b) * a.kv_cap + p] : static_cast<uint32_t>(b);
+            const size_t base = static_cast<size_t>(slot) * a.kv_slot_stride + a.kv_layer_off +
+                                (static_cast<size_t>(h) * a.kv_cap + p) * kHeadDim + sub * 4;
+            k4[i] = *reinterpret_cast<const float4*>(a.kv + base);
+            v4[i] = *reinterpret_cast<const float4*>(a.kv + base + a.kv_v_off);
+        } else {
+            k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            v4[i] = k4[i];
+        }
+    }
+    float sc[PER];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        float d = q4.x * k4[i].x;
+        d = __builtin_fmaf(q4.y, k4[i].y, d);
+        d = __builtin_fmaf(q4.z, k4[i].z, d);
+        d = __builtin_fmaf(q4.w, k4[i].w, d);
+        d += __shfl_xor(d, 1, 64);
+        d += __shfl_xor(d, 2, 64);
+        d += __shfl_xor(d, 4, 64);
+        d += __shfl_xor(d, 8, 64);
+        const bool valid = p0 + g + 16 * i < p1;
+        sc[i] = valid ? d * 0.125f : -INFINITY;
+        mloc = fmaxf(mloc, sc[i]);
+    }
+    __shared__ float redm[4], reds[4];
+    __shared__ float accs[16][kHeadDim + 4];
+    __shared__ int last;
+    const float wm = wave_max(mloc);
+    if (lane == 0) redm[wave] = wm;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+    float lsum = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const bool valid = p0 + g + 16 * i < p1;
+        const float e = valid ? expf(sc[i] - M) : 0.0f;
+        lsum += e;
+        acc.x = __builtin_fmaf(e, v4[i].x, acc.x);
+        acc.y = __builtin_fmaf(e, v4[i].y, acc.y);
+        acc.z = __builtin_fmaf(e, v4[i].z, acc.z);
+        acc.w = __builtin_fmaf(e, v4[i].w, acc.w);
+    }
+    const float ws = wave_sum(sub == 0 ? lsum : 0.0f);
+    if (lane == 0) reds[wave] = ws;
+    accs[g][sub * 4 + 0] = acc.x;
+    accs[g][sub * 4 + 1] = acc.y;
+    accs[g][sub * 4 + 2] = acc.z;
+    accs[g][sub * 4 + 3] = acc.w;
+    __syncthreads();
+    float* part = a.partial + (static_cast<size_t>(b * kHeads + h) * S + s) * 68;
+    if (t < kHeadDim) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < 16; ++gg) tot += accs[gg][t];
+        part[4 + t] = tot;
+        if (t == 0) {
+            part[0] = M;
+            part[1] = ((reds[0] + reds[1]) + reds[2]) + reds[3];
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (t == 0) last = atomicAdd(&a.ticket[b * kHeads + h], 1u) == static_cast<unsigned>(S - 1);
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    if (t < kHeadDim) {
+        const float* pb = a.partial + static_cast<size_t>(b * kHeads + h) * S * 68;
+        float mg = -INFINITY;
+        for (int k = 0; k < S; ++k) mg = fmaxf(mg, __builtin_nontemporal_load(pb + k * 68));
+        float den = 0.0f, num = 0.0f;
+        for (int k = 0; k < S; ++k) {
+            const float ms = __builtin_nontemporal_load(pb + k * 68);
+            const float wgt = ms == -INFINITY ? 0.0f : expf(ms - mg);
+            den = __builtin_fmaf(__builtin_nontemporal_load(pb + k * 68 + 1), wgt, den);
+            num = __builtin_fmaf(__builtin_nontemporal_load(pb + k * 68 + 4 + t), wgt, num);
+        }
+        a.out[b * kWidth + h * kHeadDim + t] = num / den;
+    }
+    if (t == 0) atomicExch(&a.ticket[b * kHeads + h], 0u);
+}
+
+}  // namespace
+
+int gemv_batch_bucket(int batch) {
+    for (int v : kGemvBatches)
+        if (batch <= v) return v;
+    return -1;
+}
+
+// Rows per wave: chosen so every launch has >= 320 workgroups of 4 waves.
+hipError_t launch_gemv_qkv(const GemvArgs& a, int batch, bool bf16, bool embed, hipStream_t s) {
+    return embed ? launch_gemv<kWidth, 2, kProEmbedLn, kEpiQkv>(a, batch, bf16, s)
+                 : launch_gemv<kWidth, 2, kProLn, kEpiQkv>(a, batch, bf16, s);
+}
+hipError_t launch_gemv_proj(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_gemv<kWidth, 1, kProNone, kEpiResid>(a, batch, bf16, s);
+}
+hipError_t launch_gemv_fc(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_gemv<kWidth, 2, kProLn, kEpiGelu>(a, batch, bf16, s);
+}
+hipError_t launch_gemv_fc2(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_gemv<kFfn, 1, kProNone, kEpiResid>(a, batch, bf16, s);
+}
+hipError_t launch_gemv_head(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_gemv<kWidth, 2, kProLn2, kEpiLogits>(a, batch, bf16, s);
+}
+
+hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
+    hipLaunchKernelGGL(attention_kernel, dim3(a.splits, kHeads, batch), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace itts

@@ -1,0 +1,159 @@
+// Launch-argument structs and host launch wrappers of every HIP kernel of the
+// GPT semantic-token loop.  Kernels live in decode.hip, sampler.hip, prefill.hip
+// and util.hip; the runtime (runtime.hip) only calls the wrappers below.
+#pragma once
+#include "common.h"
+
+namespace itts {
+
+// ------------------------------------------------------------------ decode GEMV
+enum Prologue : int {
+    kProNone = 0,     // x read from global as is
+    kProLn = 1,       // x = LayerNorm(x_in)
+    kProEmbedLn = 2,  // h = mel_emb[token] + mel_pos[position] (written out), x = LayerNorm(h)
+    kProLn2 = 3,      // x = LayerNorm_b(LayerNorm_a(x_in)) (ln_f then final_norm)
+};
+enum Epilogue : int {
+    kEpiQkv = 0,     // q row / K,V cache append at row n
+    kEpiResid = 1,   // out = resid + (dot + bias)
+    kEpiGelu = 2,    // out = gelu(dot + bias)
+    kEpiLogits = 3,  // out = dot + bias
+};
+
+struct GemvArgs {
+    const void* w;          // [rows][cols] row-major, fp32 or bf16
+    const float* bias;      // [rows]
+    const float* x;         // input rows [batch][x_stride]
+    int x_stride;
+    int rows;
+    const float* ln_w;      // LayerNorm (first) gamma/beta
+    const float* ln_b;
+    const float* ln2_w;     // second LayerNorm (kProLn2)
+    const float* ln2_b;
+    const float* resid;     // kEpiResid input [batch][out_stride]
+    float* out;             // [batch][out_stride]
+    int out_stride;
+    // kEpiQkv
+    float* q;               // [batch][1280]
+    float* kv;              // cache base
+    size_t kv_slot_stride;  // floats per sequence slot
+    size_t kv_layer_off;    // floats from slot base to this layer's K block
+    size_t kv_v_off;        // floats from the K block to the V block
+    uint32_t kv_cap;        // rows per (slot, layer, head)
+    // kProEmbedLn
+    const float* mel_emb;
+    const float* mel_pos;
+    float* h_out;           // [batch][1280]
+    const SeqState* state;  // [batch]
+    int nseq;               // sequences with state entries (<= batch template)
+};
+
+// Batch templates instantiated for the decode GEMVs; the runtime pads a batch up
+// to the next of these (extra slots stay inactive).
+constexpr int kGemvBatches[] = {1, 2, 3, 4, 8, 10};
+int gemv_batch_bucket(int batch);
+
+hipError_t launch_gemv_qkv(const GemvArgs& a, int batch, bool bf16, bool embed, hipStream_t s);
+hipError_t launch_gemv_proj(const GemvArgs& a, int batch, bool bf16, hipStream_t s);
+hipError_t launch_gemv_fc(const GemvArgs& a, int batch, bool bf16, hipStream_t s);
+hipError_t launch_gemv_fc2(const GemvArgs& a, int batch, bool bf16, hipStream_t s);
+hipError_t launch_gemv_head(const GemvArgs& a, int batch, bool bf16, hipStream_t s);
+
+// ------------------------------------------------------------------ decode attention
+struct AttnArgs {
+    const float* q;         // [batch][1280]
+    const float* kv;
+    size_t kv_slot_stride;
+    size_t kv_layer_off;
+    size_t kv_v_off;
+    uint32_t kv_cap;
+    const uint8_t* table;   // beam row-owner table [batch][kv_cap] (slot holding each row) or null
+    float* partial;         // [batch][20][splits][68]
+    uint32_t* ticket;       // [batch][20], zero between launches
+    float* out;             // [batch][1280]
+    const SeqState* state;
+    int nseq;               // sequences with state entries; slots >= nseq are padding
+    int splits;
+};
+constexpr int kAttnMaxChunk = 128;  // rows per split
+hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s);
+
+// ------------------------------------------------------------------ sampler
+enum SampleMode : int {
+    kModeDecode = 0,      // processors from state options + seen mask, choose, advance state
+    kModeProcessors = 1,  // processors only, write processed scores to out_scores
+    kModeDraw = 2,        // logits are already processed: draw `draws` tokens with state.rng
+};
+struct SampleArgs {
+    const float* logits;    // [batch][logit_stride]
+    int logit_stride;
+    SeqState* state;        // [batch]
+    uint8_t* seen;          // [batch][8194] repetition-penalty set
+    uint32_t* codes;        // [batch][code_stride]
+    int code_stride;
+    double* probs;          // [batch][8194] scratch
+    uint64_t* sortbuf;      // [batch][16384] scratch (large survivor sets)
+    float* out_scores;      // kModeProcessors output [batch][8194]
+    uint32_t* out_tokens;   // kModeDraw output
+    int draws;
+    int mode;
+    uint32_t* status;       // [batch] 0 ok, else error code (see sampler.hip)
+};
+hipError_t launch_sampler(const SampleArgs& a, int batch, hipStream_t s);
+
+// ------------------------------------------------------------------ prefill
+struct LnRowsArgs {
+    const float* x;
+    float* y;
+    const float* w;
+    const float* b;
+    int rows;
+};
+hipError_t launch_ln_rows(const LnRowsArgs& a, hipStream_t s);
+
+enum GemmEpi : int { kGemmQkv = 0, kGemmResid = 1, kGemmGelu = 2 };
+struct GemmArgs {
+    const float* a;         // [M][K]
+    const void* w;          // [N][K] fp32 or bf16
+    const float* bias;      // [N]
+    int M, N, K;
+    float* c;               // [M][N] (kGemmResid: read-modify-write residual)
+    // kGemmQkv: q rows to c ([M][1280]); K/V to the cache of row_slot[m] at row_pos[m]
+    float* kv;
+    size_t kv_slot_stride, kv_layer_off, kv_v_off;
+    uint32_t kv_cap;
+    const uint32_t* row_slot;
+    const uint32_t* row_pos;
+};
+hipError_t launch_gemm(const GemmArgs& a, int epi, bool bf16, hipStream_t s);
+
+struct CausalArgs {
+    const float* q;         // [M][1280]
+    const float* kv;
+    size_t kv_slot_stride, kv_layer_off, kv_v_off;
+    uint32_t kv_cap;
+    const uint32_t* row_slot;
+    const uint32_t* row_pos;
+    float* out;             // [M][1280]
+    int M;
+};
+hipError_t launch_causal_attention(const CausalArgs& a, hipStream_t s);
+
+// ------------------------------------------------------------------ utilities
+// dst[out][in] = src[in][out] (Conv1D -> row-major GEMV layout), fp32 or bf16 (RNE).
+hipError_t launch_transpose(const float* src, void* dst, int in, int out, bool bf16, hipStream_t s);
+hipError_t launch_convert(const float* src, void* dst, size_t n, bool bf16, hipStream_t s);
+// Prefix text rows (gpt.cpp:57-69): out[r] = text_emb[ids[r]] + text_pos[r] + lang_emb[lang]; last row mel start.
+hipError_t launch_text_rows(const float* text_emb, const float* text_pos, const float* lang_emb, const float* mel_emb,
+                            const float* mel_pos, const uint32_t* ids, int n_ids, uint32_t language, float* out,
+                            hipStream_t s);
+// Speaker conditioning row (gpt.cpp:53-54): out = (bias + W speaker) + emotion.
+hipError_t launch_speaker_row(const float* w, const float* b, const float* speaker, const float* emotion, float* out,
+                              hipStream_t s);
+// Copy row src_rows[b] of x into h[b] (last prefix row of each sequence).
+hipError_t launch_gather_rows(const float* x, const uint32_t* src_rows, float* h, int batch, hipStream_t s);
+// Beam reorder of the row-owner table and seen sets: child c takes parent[c]'s rows 0..n-1 and own row n.
+hipError_t launch_beam_reorder(uint8_t* table, uint8_t* table_tmp, uint8_t* seen, uint8_t* seen_tmp, const uint32_t* parent,
+                               int beams, uint32_t n, uint32_t cap, hipStream_t s);
+
+}  // namespace itts

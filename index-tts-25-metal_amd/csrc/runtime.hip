@@ -1,0 +1,1072 @@
+// Host runtime of the GPT semantic-token loop and its C ABI (include/itts_gpt.h).
+//
+// One itts_gpt handle = resident weights + KV cache slots + one HIP stream.
+//   * weights: Conv1D matrices [in][out] are transposed on the device into one slab,
+//     row-major [out][in], in consumption order (per layer: c_attn, c_proj, c_fc,
+//     mlp.c_proj; then mel_head), fp32 or bf16 (gpt.cpp:24-37 does this on the host);
+//   * KV cache: [slot][layer][K|V][head][row][64] fp32, `kv_capacity` rows per slot
+//     (gptKvCacheCreate, metal_context.mm:5675-5700, uses [layer][K|V][row][1280]);
+//   * decode: the 24-layer step (5 kernels per layer + head, + sampler) is captured once
+//     per batch bucket as a hipGraph and replayed per token.  Token, position and KV
+//     length live in device SeqState; the sampler advances them, so generate() replays
+//     the graph with no per-token host work (the reference blocks per token:
+//     gpt.cpp:123 / metal_context.mm:4613-4630).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "itts_gpt.h"
+#include "kernels.h"
+
+namespace itts {
+namespace {
+
+thread_local std::string g_create_error;
+
+#define HIP_CHECK(x)                                                                                         \
+    do {                                                                                                     \
+        const hipError_t e_ = (x);                                                                           \
+        if (e_ != hipSuccess) throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(e_) + " in " #x); \
+    } while (0)
+
+template <class T>
+struct DevBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { reset(); }
+    void reset() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void alloc(size_t count) {
+        reset();
+        if (count) HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
+        n = count;
+    }
+    void ensure(size_t count) {
+        if (count > n) alloc(count);
+    }
+};
+
+struct HostTensor {
+    const float* data;
+    std::vector<int64_t> shape;
+};
+
+// Status codes written by the sampler (sampler.hip).
+const char* sampler_message(uint32_t s) {
+    switch (s) {
+        case 1: return "GPT top_p filtering removed all logits";
+        case 2: return "GPT sampling probability mass is zero";
+        case 3: return "GPT sampling received no finite logits";
+        case 4: return "GPT generated invalid semantic code";
+        default: return "GPT sampler failed";
+    }
+}
+
+struct Snapshot {
+    uint32_t tokens = 0;
+    DevBuf<float> kv;
+};
+
+}  // namespace
+
+struct Engine {
+    // ---------------------------------------------------------------- model
+    int layers = 0;
+    uint32_t text_vocab = 0, text_pos_rows = 0, lang_vocab = 0, mel_pos_rows = 0;
+    bool bf16 = false;
+    uint32_t cap = 4096, max_batch = 1;
+    DevBuf<uint8_t> slab;  // GEMV weights
+    size_t elt = 4;
+    std::vector<size_t> off_qkv, off_proj, off_fc, off_fc2;  // element offsets
+    size_t off_head = 0;
+    DevBuf<float> params, head_params, text_emb, text_pos, lang_emb, mel_emb, mel_pos, spk_w, spk_b;
+    bool has_speaker = false;
+
+    // ---------------------------------------------------------------- sequences
+    hipStream_t stream = nullptr;
+    DevBuf<float> kv;
+    size_t kv_slot_stride = 0, kv_layer_stride = 0, kv_v_off = 0;
+    DevBuf<float> h, hmid, q, attn, ff, logits, partial;
+    DevBuf<uint32_t> ticket, codes, status, d_parent;
+    DevBuf<SeqState> state;  // kMaxBatch + 1 entries; the last one serves the processor/sampler API
+    DevBuf<uint8_t> seen, seen_tmp, table, table_tmp;
+    DevBuf<double> probs;
+    // prefill scratch
+    DevBuf<float> px, pxn, pq, patt, pff;
+    DevBuf<uint32_t> row_slot, row_pos, last_rows;
+    // API scratch
+    DevBuf<float> api_out;
+    DevBuf<uint32_t> api_tokens;
+    uint32_t* pinned = nullptr;  // host pinned staging (flags)
+    SeqState* pinned_state = nullptr;
+    int splits = 16;
+    std::map<std::tuple<int, int, bool, bool>, hipGraphExec_t> graphs;
+    hipEvent_t ev[4] = {};
+    uint32_t cached = 0;
+    itts_gpt_timing timing{};
+    std::string last_error;
+
+    ~Engine() {
+        for (auto& kvp : graphs) (void)hipGraphExecDestroy(kvp.second);
+        for (auto& e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (pinned) (void)hipHostFree(pinned);
+        if (pinned_state) (void)hipHostFree(pinned_state);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    void* w_ptr(size_t off) const { return slab.p + off * elt; }
+    size_t kv_layer_off(int l) const { return static_cast<size_t>(l) * kv_layer_stride; }
+
+    // ---------------------------------------------------------------- construction
+    // Stream, events and the sampler/processor buffers (all a sampler-only handle needs).
+    void init_common() {
+        HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+        for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+        HIP_CHECK(hipHostMalloc(&pinned, 64 * sizeof(uint32_t), hipHostMallocDefault));
+        HIP_CHECK(hipHostMalloc(&pinned_state, (kMaxBatch + 1) * sizeof(SeqState), hipHostMallocDefault));
+        const size_t B = kMaxBatch;
+        logits.alloc((B + 1) * kMelVocab);
+        status.alloc(B + 1);
+        state.alloc(B + 1);
+        HIP_CHECK(hipMemsetAsync(state.p, 0, state.n * sizeof(SeqState), stream));
+        seen.alloc((B + 1) * kMelVocab);
+        probs.alloc((B + 1) * kMelVocab);
+        api_out.alloc(kMelVocab);
+        api_tokens.alloc(1 << 16);
+        HIP_CHECK(hipStreamSynchronize(stream));
+    }
+
+    void create(const itts_tensor* tensors, int32_t count, const itts_gpt_config* cfg) {
+        init_common();
+        if (count == 0) return;  // sampler-only handle
+        std::unordered_map<std::string, HostTensor> by;
+        for (int32_t i = 0; i < count; ++i)
+            by[tensors[i].name] = HostTensor{tensors[i].data, std::vector<int64_t>(tensors[i].shape, tensors[i].shape + tensors[i].ndim)};
+        auto info = [&](const std::string& name) -> const HostTensor& {
+            auto it = by.find(name);
+            if (it == by.end()) throw std::runtime_error("Missing tensor: " + name);
+            return it->second;
+        };
+        // gpt.cpp:9-11: shape checks; vocabulary/position table sizes come from the tensors.
+        auto check = [&](const std::string& name, const std::vector<int64_t>& shape) -> const float* {
+            const auto& t = info(name);
+            if (t.shape != shape) throw std::runtime_error("Unsupported 2.5 GPT shape: " + name);
+            return t.data;
+        };
+        auto rows_of = [&](const std::string& name) -> uint32_t {
+            const auto& t = info(name);
+            if (t.shape.size() != 2 || t.shape[1] != kWidth || t.shape[0] <= 0)
+                throw std::runtime_error("Unsupported 2.5 GPT shape: " + name);
+            return static_cast<uint32_t>(t.shape[0]);
+        };
+        cap = cfg && cfg->kv_capacity ? cfg->kv_capacity : 4096;
+        max_batch = cfg && cfg->max_batch ? cfg->max_batch : 1;
+        bf16 = cfg && cfg->weight_dtype == ITTS_WEIGHTS_BF16;
+        if (cfg && cfg->weight_dtype > ITTS_WEIGHTS_BF16) throw std::invalid_argument("Unknown weight dtype");
+        if (max_batch > static_cast<uint32_t>(kMaxBatch)) throw std::invalid_argument("max_batch exceeds 10");
+        if (cap < 2 || cap > 65536) throw std::invalid_argument("Invalid KV capacity");
+        elt = bf16 ? 2 : 4;
+
+        text_vocab = rows_of("gpt.text_embedding.weight");
+        text_pos_rows = rows_of("gpt.text_pos_embedding.emb.weight");
+        lang_vocab = rows_of("gpt.lang_embedding.weight");
+        mel_pos_rows = rows_of("gpt.mel_pos_embedding.emb.weight");
+        check("gpt.mel_embedding.weight", {kMelVocab, kWidth});
+        has_speaker = by.count("gpt.spk_emb_proj.weight") != 0;
+        if (has_speaker) check("gpt.spk_emb_proj.weight", {kWidth, 192});
+        while (by.count("gpt.gpt.h." + std::to_string(layers) + ".attn.c_attn.weight")) ++layers;
+        if (!layers) throw std::runtime_error("Missing tensor: gpt.gpt.h.0.attn.c_attn.weight");
+
+        // Weight slab.
+        const size_t per_layer = static_cast<size_t>(kQkv) * kWidth + static_cast<size_t>(kWidth) * kWidth +
+                                 2 * static_cast<size_t>(kFfn) * kWidth;
+        const size_t total = per_layer * layers + static_cast<size_t>(kMelVocab) * kWidth;
+        slab.alloc(total * elt);
+        DevBuf<float> staging;
+        staging.alloc(static_cast<size_t>(kMelVocab) * kWidth);
+        auto upload = [&](const float* src, size_t n, float* dst) {
+            HIP_CHECK(hipMemcpyAsync(dst, src, n * 4, hipMemcpyHostToDevice, stream));
+        };
+        auto put_conv = [&](const std::string& name, int in, int out, size_t off) {
+            const float* src = check(name, {in, out});
+            upload(src, static_cast<size_t>(in) * out, staging.p);
+            HIP_CHECK(launch_transpose(staging.p, w_ptr(off), in, out, bf16, stream));
+            HIP_CHECK(hipStreamSynchronize(stream));  // staging is reused
+        };
+        params.alloc(static_cast<size_t>(layers) * kParLayer);
+        std::vector<float> par(static_cast<size_t>(layers) * kParLayer);
+        size_t off = 0;
+        for (int l = 0; l < layers; ++l) {
+            const std::string p = "gpt.gpt.h." + std::to_string(l);
+            off_qkv.push_back(off);
+            put_conv(p + ".attn.c_attn.weight", kWidth, kQkv, off);
+            off += static_cast<size_t>(kQkv) * kWidth;
+            off_proj.push_back(off);
+            put_conv(p + ".attn.c_proj.weight", kWidth, kWidth, off);
+            off += static_cast<size_t>(kWidth) * kWidth;
+            off_fc.push_back(off);
+            put_conv(p + ".mlp.c_fc.weight", kWidth, kFfn, off);
+            off += static_cast<size_t>(kFfn) * kWidth;
+            off_fc2.push_back(off);
+            put_conv(p + ".mlp.c_proj.weight", kFfn, kWidth, off);
+            off += static_cast<size_t>(kFfn) * kWidth;
+            float* dst = &par[static_cast<size_t>(l) * kParLayer];
+            auto cp = [&](const std::string& name, int n, int at) { std::memcpy(dst + at, check(name, {n}), n * 4); };
+            cp(p + ".ln_1.weight", kWidth, kParLn1W);
+            cp(p + ".ln_1.bias", kWidth, kParLn1B);
+            cp(p + ".attn.c_attn.bias", kQkv, kParQkvB);
+            cp(p + ".attn.c_proj.bias", kWidth, kParProjB);
+            cp(p + ".ln_2.weight", kWidth, kParLn2W);
+            cp(p + ".ln_2.bias", kWidth, kParLn2B);
+            cp(p + ".mlp.c_fc.bias", kFfn, kParFcB);
+            cp(p + ".mlp.c_proj.bias", kWidth, kParFc2B);
+        }
+        off_head = off;
+        upload(check("gpt.mel_head.weight", {kMelVocab, kWidth}), static_cast<size_t>(kMelVocab) * kWidth, staging.p);
+        HIP_CHECK(launch_convert(staging.p, w_ptr(off_head), static_cast<size_t>(kMelVocab) * kWidth, bf16, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        upload(par.data(), par.size(), params.p);
+        std::vector<float> hp(kHeadPar);
+        std::memcpy(&hp[kHeadLnfW], check("gpt.gpt.ln_f.weight", {kWidth}), kWidth * 4);
+        std::memcpy(&hp[kHeadLnfB], check("gpt.gpt.ln_f.bias", {kWidth}), kWidth * 4);
+        std::memcpy(&hp[kHeadFnW], check("gpt.final_norm.weight", {kWidth}), kWidth * 4);
+        std::memcpy(&hp[kHeadFnB], check("gpt.final_norm.bias", {kWidth}), kWidth * 4);
+        std::memcpy(&hp[kHeadBias], check("gpt.mel_head.bias", {kMelVocab}), kMelVocab * 4);
+        head_params.alloc(kHeadPar);
+        upload(hp.data(), hp.size(), head_params.p);
+        auto table_up = [&](DevBuf<float>& d, const std::string& name, uint32_t rows) {
+            d.alloc(static_cast<size_t>(rows) * kWidth);
+            upload(info(name).data, d.n, d.p);
+        };
+        table_up(text_emb, "gpt.text_embedding.weight", text_vocab);
+        table_up(text_pos, "gpt.text_pos_embedding.emb.weight", text_pos_rows);
+        table_up(lang_emb, "gpt.lang_embedding.weight", lang_vocab);
+        table_up(mel_emb, "gpt.mel_embedding.weight", kMelVocab);
+        table_up(mel_pos, "gpt.mel_pos_embedding.emb.weight", mel_pos_rows);
+        if (has_speaker) {
+            spk_w.alloc(static_cast<size_t>(kWidth) * 192);
+            upload(info("gpt.spk_emb_proj.weight").data, spk_w.n, spk_w.p);
+            spk_b.alloc(kWidth);
+            upload(check("gpt.spk_emb_proj.bias", {kWidth}), kWidth, spk_b.p);
+        }
+
+        // KV cache and decode buffers.
+        kv_layer_stride = 2ull * kHeads * cap * kHeadDim;
+        kv_v_off = static_cast<size_t>(kHeads) * cap * kHeadDim;
+        kv_slot_stride = kv_layer_stride * layers;
+        kv.alloc(kv_slot_stride * max_batch);
+        const size_t B = kMaxBatch;
+        h.alloc(B * kWidth);
+        hmid.alloc(B * kWidth);
+        q.alloc(B * kWidth);
+        attn.alloc(B * kWidth);
+        ff.alloc(B * kFfn);
+        splits = std::max<int>(16, (cap + kAttnMaxChunk - 1) / kAttnMaxChunk);
+        partial.alloc(B * kHeads * splits * 68);
+        ticket.alloc(B * kHeads);
+        HIP_CHECK(hipMemsetAsync(ticket.p, 0, ticket.n * 4, stream));
+        codes.alloc((B + 1) * cap);
+        d_parent.alloc(B);
+        seen_tmp.alloc((B + 1) * kMelVocab);
+        table.alloc(B * cap);
+        table_tmp.alloc(B * cap);
+        HIP_CHECK(hipStreamSynchronize(stream));
+    }
+
+    // ---------------------------------------------------------------- forward pieces
+    GemvArgs gemv_base(int nseq) const {
+        GemvArgs a{};
+        a.state = state.p;
+        a.nseq = nseq;
+        a.kv = kv.p;
+        a.kv_slot_stride = kv_slot_stride;
+        a.kv_v_off = kv_v_off;
+        a.kv_cap = cap;
+        return a;
+    }
+
+    // One decode step for sequences 0..nseq-1 (state-driven), padded to batch bucket nb.
+    void enqueue_forward(int nseq, int nb, bool use_table) {
+        for (int l = 0; l < layers; ++l) {
+            const float* par = params.p + static_cast<size_t>(l) * kParLayer;
+            GemvArgs a = gemv_base(nseq);
+            a.w = w_ptr(off_qkv[l]);
+            a.bias = par + kParQkvB;
+            a.rows = kQkv;
+            a.x = h.p;
+            a.x_stride = kWidth;
+            a.ln_w = par + kParLn1W;
+            a.ln_b = par + kParLn1B;
+            a.q = q.p;
+            a.kv_layer_off = kv_layer_off(l);
+            a.mel_emb = mel_emb.p;
+            a.mel_pos = mel_pos.p;
+            a.h_out = h.p;
+            HIP_CHECK(launch_gemv_qkv(a, nb, bf16, l == 0, stream));
+
+            AttnArgs t{};
+            t.q = q.p;
+            t.kv = kv.p;
+            t.kv_slot_stride = kv_slot_stride;
+            t.kv_layer_off = kv_layer_off(l);
+            t.kv_v_off = kv_v_off;
+            t.kv_cap = cap;
+            t.table = use_table ? table.p : nullptr;
+            t.partial = partial.p;
+            t.ticket = ticket.p;
+            t.out = attn.p;
+            t.state = state.p;
+            t.nseq = nseq;
+            t.splits = splits;
+            HIP_CHECK(launch_attention(t, nb, stream));
+
+            GemvArgs p = gemv_base(nseq);
+            p.w = w_ptr(off_proj[l]);
+            p.bias = par + kParProjB;
+            p.rows = kWidth;
+            p.x = attn.p;
+            p.x_stride = kWidth;
+            p.resid = h.p;
+            p.out = hmid.p;
+            p.out_stride = kWidth;
+            HIP_CHECK(launch_gemv_proj(p, nb, bf16, stream));
+
+            GemvArgs f = gemv_base(nseq);
+            f.w = w_ptr(off_fc[l]);
+            f.bias = par + kParFcB;
+            f.rows = kFfn;
+            f.x = hmid.p;
+            f.x_stride = kWidth;
+            f.ln_w = par + kParLn2W;
+            f.ln_b = par + kParLn2B;
+            f.out = ff.p;
+            f.out_stride = kFfn;
+            HIP_CHECK(launch_gemv_fc(f, nb, bf16, stream));
+
+            GemvArgs g = gemv_base(nseq);
+            g.w = w_ptr(off_fc2[l]);
+            g.bias = par + kParFc2B;
+            g.rows = kWidth;
+            g.x = ff.p;
+            g.x_stride = kFfn;
+            g.resid = hmid.p;
+            g.out = h.p;
+            g.out_stride = kWidth;
+            HIP_CHECK(launch_gemv_fc2(g, nb, bf16, stream));
+        }
+        enqueue_head(nseq, nb);
+    }
+
+    void enqueue_head(int nseq, int nb) {
+        GemvArgs a = gemv_base(nseq);
+        a.w = w_ptr(off_head);
+        a.bias = head_params.p + kHeadBias;
+        a.rows = kMelVocab;
+        a.x = h.p;
+        a.x_stride = kWidth;
+        a.ln_w = head_params.p + kHeadLnfW;
+        a.ln_b = head_params.p + kHeadLnfB;
+        a.ln2_w = head_params.p + kHeadFnW;
+        a.ln2_b = head_params.p + kHeadFnB;
+        a.out = logits.p;
+        a.out_stride = kMelVocab;
+        HIP_CHECK(launch_gemv_head(a, nb, bf16, stream));
+    }
+
+    SampleArgs sample_base(int mode) {
+        SampleArgs s{};
+        s.logits = logits.p;
+        s.logit_stride = kMelVocab;
+        s.state = state.p;
+        s.seen = seen.p;
+        s.codes = codes.p;
+        s.code_stride = static_cast<int>(cap);
+        s.probs = probs.p;
+        s.status = status.p;
+        s.mode = mode;
+        return s;
+    }
+
+    hipGraphExec_t graph(int nseq, int nb, bool sampler, bool use_table) {
+        const auto key = std::make_tuple(nseq, nb, sampler, use_table);
+        auto it = graphs.find(key);
+        if (it != graphs.end()) return it->second;
+        hipGraph_t g = nullptr;
+        HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+        try {
+            enqueue_forward(nseq, nb, use_table);
+            if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
+        } catch (...) {
+            (void)hipStreamEndCapture(stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        HIP_CHECK(hipStreamEndCapture(stream, &g));
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        HIP_CHECK(e);
+        graphs[key] = exec;
+        return exec;
+    }
+
+    // ---------------------------------------------------------------- prefill
+    // Stacked prefill of several sequences (slot b <- prefixes[b], rows[b] rows each).
+    void enqueue_prefill(const std::vector<const float*>& prefixes, const std::vector<uint32_t>& rows) {
+        const int nseq = static_cast<int>(prefixes.size());
+        uint32_t M = 0;
+        for (auto r : rows) M += r;
+        px.ensure(static_cast<size_t>(M) * kWidth);
+        pxn.ensure(static_cast<size_t>(M) * kWidth);
+        pq.ensure(static_cast<size_t>(M) * kWidth);
+        patt.ensure(static_cast<size_t>(M) * kWidth);
+        pff.ensure(static_cast<size_t>(M) * kFfn);
+        row_slot.ensure(M);
+        row_pos.ensure(M);
+        last_rows.ensure(kMaxBatch);
+        std::vector<uint32_t> slot(M), pos(M), last(kMaxBatch, 0);
+        uint32_t m = 0;
+        for (int b = 0; b < nseq; ++b) {
+            HIP_CHECK(hipMemcpyAsync(px.p + static_cast<size_t>(m) * kWidth, prefixes[b], static_cast<size_t>(rows[b]) * kWidth * 4,
+                                     hipMemcpyHostToDevice, stream));
+            for (uint32_t r = 0; r < rows[b]; ++r) {
+                slot[m + r] = static_cast<uint32_t>(b);
+                pos[m + r] = r;
+            }
+            m += rows[b];
+            last[b] = m - 1;
+        }
+        HIP_CHECK(hipMemcpyAsync(row_slot.p, slot.data(), M * 4, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(row_pos.p, pos.data(), M * 4, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(last_rows.p, last.data(), kMaxBatch * 4, hipMemcpyHostToDevice, stream));
+        // Host vectors above must outlive the async copies.
+        HIP_CHECK(hipStreamSynchronize(stream));
+        for (int l = 0; l < layers; ++l) {
+            const float* par = params.p + static_cast<size_t>(l) * kParLayer;
+            HIP_CHECK(launch_ln_rows(LnRowsArgs{px.p, pxn.p, par + kParLn1W, par + kParLn1B, static_cast<int>(M)}, stream));
+            GemmArgs g{};
+            g.a = pxn.p;
+            g.w = w_ptr(off_qkv[l]);
+            g.bias = par + kParQkvB;
+            g.M = static_cast<int>(M);
+            g.N = kQkv;
+            g.K = kWidth;
+            g.c = pq.p;
+            g.kv = kv.p;
+            g.kv_slot_stride = kv_slot_stride;
+            g.kv_layer_off = kv_layer_off(l);
+            g.kv_v_off = kv_v_off;
+            g.kv_cap = cap;
+            g.row_slot = row_slot.p;
+            g.row_pos = row_pos.p;
+            HIP_CHECK(launch_gemm(g, kGemmQkv, bf16, stream));
+            CausalArgs c{};
+            c.q = pq.p;
+            c.kv = kv.p;
+            c.kv_slot_stride = kv_slot_stride;
+            c.kv_layer_off = kv_layer_off(l);
+            c.kv_v_off = kv_v_off;
+            c.kv_cap = cap;
+            c.row_slot = row_slot.p;
+            c.row_pos = row_pos.p;
+            c.out = patt.p;
+            c.M = static_cast<int>(M);
+            HIP_CHECK(launch_causal_attention(c, stream));
+            GemmArgs p{};
+            p.a = patt.p;
+            p.w = w_ptr(off_proj[l]);
+            p.bias = par + kParProjB;
+            p.M = static_cast<int>(M);
+            p.N = kWidth;
+            p.K = kWidth;
+            p.c = px.p;
+            HIP_CHECK(launch_gemm(p, kGemmResid, bf16, stream));
+            HIP_CHECK(launch_ln_rows(LnRowsArgs{px.p, pxn.p, par + kParLn2W, par + kParLn2B, static_cast<int>(M)}, stream));
+            GemmArgs f{};
+            f.a = pxn.p;
+            f.w = w_ptr(off_fc[l]);
+            f.bias = par + kParFcB;
+            f.M = static_cast<int>(M);
+            f.N = kFfn;
+            f.K = kWidth;
+            f.c = pff.p;
+            HIP_CHECK(launch_gemm(f, kGemmGelu, bf16, stream));
+            GemmArgs f2{};
+            f2.a = pff.p;
+            f2.w = w_ptr(off_fc2[l]);
+            f2.bias = par + kParFc2B;
+            f2.M = static_cast<int>(M);
+            f2.N = kWidth;
+            f2.K = kFfn;
+            f2.c = px.p;
+            HIP_CHECK(launch_gemm(f2, kGemmResid, bf16, stream));
+        }
+        HIP_CHECK(launch_gather_rows(px.p, last_rows.p, h.p, nseq, stream));
+        enqueue_head(nseq, gemv_batch_bucket(nseq));
+    }
+
+    void upload_states(int n) {
+        HIP_CHECK(hipMemcpyAsync(state.p, pinned_state, n * sizeof(SeqState), hipMemcpyHostToDevice, stream));
+    }
+
+    static SeqState make_state(const itts_gen_options& o, uint32_t prefix_rows, uint32_t max_tokens) {
+        SeqState s{};
+        s.n = prefix_rows;
+        s.active = 1;
+        s.max_tokens = max_tokens;
+        s.prefix_rows = prefix_rows;
+        s.do_sample = o.do_sample ? 1u : 0u;
+        s.top_k = o.top_k;
+        s.num_beams = o.num_beams;
+        s.temperature = o.temperature;
+        s.top_p = o.top_p;
+        s.penalty = o.repetition_penalty;
+        s.suppress_stop = o.suppress_stop;
+        s.rng = o.seed;
+        return s;
+    }
+
+    // ---------------------------------------------------------------- API operations
+    void check_prefix(uint32_t rows) const {
+        if (rows == 0 || rows > 1024 || rows > cap) throw std::invalid_argument("Invalid GPT prefill dimensions");
+    }
+
+    void prefill(const float* prefix, uint32_t rows, float* out_logits) {
+        check_prefix(rows);
+        itts_gen_options o;
+        itts_gen_options_default(&o);
+        pinned_state[0] = make_state(o, rows, 1);
+        upload_states(1);
+        HIP_CHECK(hipEventRecord(ev[0], stream));
+        enqueue_prefill({prefix}, {rows});
+        HIP_CHECK(hipEventRecord(ev[1], stream));
+        HIP_CHECK(hipMemcpyAsync(out_logits, logits.p, kMelVocab * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        HIP_CHECK(hipEventElapsedTime(&timing.prefill_ms, ev[0], ev[1]));
+        cached = rows;
+    }
+
+    void step(uint32_t code, uint32_t position, float* out_logits) {
+        if (!cached || cached >= cap || code >= static_cast<uint32_t>(kMelVocab) || position >= mel_pos_rows)
+            throw std::invalid_argument("GPT step requires valid cache, code and position");
+        itts_gen_options o;
+        itts_gen_options_default(&o);
+        SeqState s = make_state(o, cached, 1);
+        s.n = cached;
+        s.token = code;
+        s.position = position;
+        pinned_state[0] = s;
+        upload_states(1);
+        HIP_CHECK(hipGraphLaunch(graph(1, 1, false, false), stream));
+        HIP_CHECK(hipMemcpyAsync(out_logits, logits.p, kMelVocab * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        cached++;
+    }
+
+    static void validate_generation(itts_gen_options& c, uint32_t maximum, uint32_t prefix_rows, uint32_t mel_rows, uint32_t cap) {
+        // gpt_sampling.cpp:169-173 (the reference's literal 1280 and 4096 are width and capacity).
+        if (!maximum || maximum + 1 >= mel_rows || prefix_rows + maximum >= cap)
+            throw std::invalid_argument("GPT generation capacity exceeded");
+        if (!c.do_sample) {
+            c.temperature = 1;
+            c.top_k = 0;
+            c.top_p = 1;
+        }
+        if (!std::isfinite(c.temperature) || !std::isfinite(c.top_p) || !std::isfinite(c.repetition_penalty) || c.temperature <= 0 ||
+            c.top_p <= 0 || c.top_p > 1 || c.repetition_penalty <= 0)
+            throw std::invalid_argument("Invalid GPT generation parameters");
+        if (!c.num_beams || c.num_beams > 10 || !std::isfinite(c.length_penalty))
+            throw std::invalid_argument("Invalid beam search configuration");
+    }
+
+    void reset_seen(int nseq) {
+        std::vector<uint8_t> s(static_cast<size_t>(nseq) * kMelVocab, 0);
+        for (int b = 0; b < nseq; ++b) {
+            s[static_cast<size_t>(b) * kMelVocab + 1] = 1;  // history {1, 8192} (gpt_sampling.cpp:176)
+            s[static_cast<size_t>(b) * kMelVocab + kMelStart] = 1;
+        }
+        HIP_CHECK(hipMemcpyAsync(seen.p, s.data(), s.size(), hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+    }
+
+    // Device-driven decode loop for nseq independent sequences whose prefill logits
+    // are in logits[0..nseq): sampler, then (forward + sampler) graph replays.
+    void decode_loop(int nseq, uint32_t max_tokens) {
+        const int nb = gemv_batch_bucket(nseq);
+        const hipGraphExec_t g = graph(nseq, nb, true, false);  // captured before any work is queued
+        HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
+        constexpr uint32_t kChunk = 16;
+        uint32_t launched = 0;
+        int k = 0;
+        while (launched + 1 < max_tokens) {
+            const uint32_t n = std::min(kChunk, max_tokens - 1 - launched);
+            for (uint32_t i = 0; i < n; ++i) HIP_CHECK(hipGraphLaunch(g, stream));
+            launched += n;
+            HIP_CHECK(hipMemcpyAsync(pinned + 16 * (k & 1), &state.p[0].active, 4, hipMemcpyDeviceToHost, stream));
+            for (int b = 1; b < nseq; ++b)
+                HIP_CHECK(hipMemcpyAsync(pinned + 16 * (k & 1) + b, &state.p[b].active, 4, hipMemcpyDeviceToHost, stream));
+            HIP_CHECK(hipEventRecord(ev[2 + (k & 1)], stream));
+            if (k >= 1) {
+                HIP_CHECK(hipEventSynchronize(ev[2 + ((k - 1) & 1)]));
+                bool any = false;
+                for (int b = 0; b < nseq; ++b) any |= pinned[16 * ((k - 1) & 1) + b] != 0;
+                if (!any) break;
+            }
+            ++k;
+        }
+    }
+
+    void generate_batch(const std::vector<const float*>& prefixes, const std::vector<uint32_t>& rows,
+                        const std::vector<itts_gen_options>& opts_in, uint32_t max_tokens, uint32_t* codes_out,
+                        uint32_t* n_codes, int32_t* stopped) {
+        const int nseq = static_cast<int>(prefixes.size());
+        if (nseq < 1 || static_cast<uint32_t>(nseq) > max_batch) throw std::invalid_argument("Invalid batch size");
+        std::vector<itts_gen_options> opts = opts_in;
+        for (int b = 0; b < nseq; ++b) {
+            check_prefix(rows[b]);
+            validate_generation(opts[b], max_tokens, rows[b], mel_pos_rows, cap);
+            if (opts[b].num_beams > 1) throw std::invalid_argument("Beam search is decoded one request at a time");
+        }
+        for (int b = 0; b < nseq; ++b) pinned_state[b] = make_state(opts[b], rows[b], max_tokens);
+        upload_states(nseq);
+        reset_seen(nseq);
+        HIP_CHECK(hipEventRecord(ev[0], stream));
+        enqueue_prefill(prefixes, rows);
+        HIP_CHECK(hipEventRecord(ev[1], stream));
+        decode_loop(nseq, max_tokens);
+        HIP_CHECK(hipEventRecord(ev[2], stream));
+        HIP_CHECK(hipMemcpyAsync(pinned_state, state.p, nseq * sizeof(SeqState), hipMemcpyDeviceToHost, stream));
+        std::vector<uint32_t> st(nseq);
+        HIP_CHECK(hipMemcpyAsync(st.data(), status.p, nseq * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        HIP_CHECK(hipEventElapsedTime(&timing.prefill_ms, ev[0], ev[1]));
+        HIP_CHECK(hipEventElapsedTime(&timing.decode_ms, ev[1], ev[2]));
+        uint32_t steps = 0;
+        for (int b = 0; b < nseq; ++b) {
+            const SeqState& s = pinned_state[b];
+            if (s.error) throw std::runtime_error(sampler_message(st[b]));
+            steps = std::max(steps, s.count);
+            HIP_CHECK(hipMemcpy(codes_out + static_cast<size_t>(b) * max_tokens, codes.p + static_cast<size_t>(b) * cap,
+                                s.count * 4, hipMemcpyDeviceToHost));
+            n_codes[b] = s.count;
+            stopped[b] = s.stopped ? 1 : 0;
+        }
+        timing.decode_steps = steps;
+        const SeqState& s0 = pinned_state[0];
+        cached = s0.prefix_rows + (s0.stopped ? s0.count : (s0.count ? s0.count - 1 : 0));
+    }
+
+    void generate(const float* prefix, uint32_t rows, const itts_gen_options& opt, uint32_t max_tokens, uint32_t* codes_out,
+                  uint32_t* n_codes, int32_t* stopped);
+
+    // ---------------------------------------------------------------- processors / sampler API
+    void apply_processors(const float* in, uint32_t vocab, const uint32_t* history, uint32_t n_history,
+                          const itts_gen_options& o, float* out) {
+        if (vocab != static_cast<uint32_t>(kMelVocab)) throw std::invalid_argument("Processors run on the 8194-entry mel vocabulary");
+        // Argument checks in the reference's order (gpt_sampling.cpp:33-35, 50-52, 69-71).
+        if (o.repetition_penalty != 1.0f && o.repetition_penalty <= 0.0f)
+            throw std::runtime_error("GPT repetition penalty must be positive");
+        if (o.temperature <= 0.0f) throw std::runtime_error("GPT sampling temperature must be positive");
+        if (o.top_p < 1.0f && o.top_p <= 0.0f) throw std::runtime_error("GPT top_p must be in (0, 1]");
+        const int slot = kMaxBatch;
+        std::vector<uint8_t> sn(kMelVocab, 0);
+        for (uint32_t i = 0; i < n_history; ++i)
+            if (history[i] < vocab) sn[history[i]] = 1;
+        SeqState s = make_state(o, 0, 0);
+        pinned_state[slot] = s;
+        HIP_CHECK(hipMemcpyAsync(state.p + slot, pinned_state + slot, sizeof(SeqState), hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(seen.p + static_cast<size_t>(slot) * kMelVocab, sn.data(), kMelVocab, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(logits.p + static_cast<size_t>(slot) * kMelVocab, in, kMelVocab * 4, hipMemcpyHostToDevice, stream));
+        SampleArgs a = sample_base(kModeProcessors);
+        a.logits = logits.p + static_cast<size_t>(slot) * kMelVocab;
+        a.state = state.p + slot;
+        a.seen = seen.p + static_cast<size_t>(slot) * kMelVocab;
+        a.probs = probs.p + static_cast<size_t>(slot) * kMelVocab;
+        a.status = status.p + slot;
+        a.out_scores = api_out.p;
+        HIP_CHECK(launch_sampler(a, 1, stream));
+        uint32_t st = 0;
+        HIP_CHECK(hipMemcpyAsync(out, api_out.p, kMelVocab * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipMemcpyAsync(&st, status.p + slot, 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        if (st) throw std::runtime_error(sampler_message(st));
+    }
+
+    void sample(const float* processed, uint32_t vocab, uint64_t* rng, uint32_t draws, uint32_t* tokens) {
+        if (vocab != static_cast<uint32_t>(kMelVocab)) throw std::invalid_argument("Sampler runs on the 8194-entry mel vocabulary");
+        if (draws == 0 || draws > api_tokens.n) throw std::invalid_argument("Invalid draw count");
+        const int slot = kMaxBatch;
+        itts_gen_options o;
+        itts_gen_options_default(&o);
+        SeqState s = make_state(o, 0, 0);
+        s.rng = *rng;
+        pinned_state[slot] = s;
+        HIP_CHECK(hipMemcpyAsync(state.p + slot, pinned_state + slot, sizeof(SeqState), hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(logits.p + static_cast<size_t>(slot) * kMelVocab, processed, kMelVocab * 4, hipMemcpyHostToDevice, stream));
+        SampleArgs a = sample_base(kModeDraw);
+        a.logits = logits.p + static_cast<size_t>(slot) * kMelVocab;
+        a.state = state.p + slot;
+        a.seen = seen.p + static_cast<size_t>(slot) * kMelVocab;
+        a.probs = probs.p + static_cast<size_t>(slot) * kMelVocab;
+        a.status = status.p + slot;
+        a.out_tokens = api_tokens.p;
+        a.draws = static_cast<int>(draws);
+        HIP_CHECK(launch_sampler(a, 1, stream));
+        uint32_t st = 0;
+        HIP_CHECK(hipMemcpyAsync(tokens, api_tokens.p, draws * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipMemcpyAsync(&st, status.p + slot, 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipMemcpyAsync(pinned_state + slot, state.p + slot, sizeof(SeqState), hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        if (st) throw std::runtime_error(sampler_message(st));
+        *rng = pinned_state[slot].rng;
+    }
+
+    // ---------------------------------------------------------------- checkpoint / restore
+    Snapshot* checkpoint() {
+        if (!cached || cached > cap) throw std::invalid_argument("Invalid KV snapshot");
+        auto s = std::make_unique<Snapshot>();
+        s->tokens = cached;
+        const size_t blocks = static_cast<size_t>(layers) * 2 * kHeads;
+        s->kv.alloc(blocks * cached * kHeadDim);
+        HIP_CHECK(hipMemcpy2DAsync(s->kv.p, static_cast<size_t>(cached) * kHeadDim * 4, kv.p, static_cast<size_t>(cap) * kHeadDim * 4,
+                                   static_cast<size_t>(cached) * kHeadDim * 4, blocks, hipMemcpyDeviceToDevice, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        return s.release();
+    }
+    void restore(const Snapshot& s) {
+        if (!s.tokens || s.tokens > cap) throw std::invalid_argument("Invalid KV restore");
+        const size_t blocks = static_cast<size_t>(layers) * 2 * kHeads;
+        HIP_CHECK(hipMemcpy2DAsync(kv.p, static_cast<size_t>(cap) * kHeadDim * 4, s.kv.p, static_cast<size_t>(s.tokens) * kHeadDim * 4,
+                                   static_cast<size_t>(s.tokens) * kHeadDim * 4, blocks, hipMemcpyDeviceToDevice, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        cached = s.tokens;
+    }
+
+    // ---------------------------------------------------------------- prefix
+    void prepare_tail(const uint32_t* text, uint32_t n_text, uint32_t language, std::vector<uint32_t>& ids) {
+        if (language >= lang_vocab) throw std::invalid_argument("Invalid GPT conditioning dimensions");
+        ids.assign(1, 0u);
+        for (uint32_t i = 0; i < n_text; ++i) {
+            if (text[i] >= text_vocab) throw std::invalid_argument("Text token is outside 2.5 vocabulary");
+            if (text[i] != 0 && text[i] != 1) ids.push_back(text[i]);
+        }
+        ids.push_back(1);
+        if (ids.size() > text_pos_rows) throw std::invalid_argument("Text segment exceeds GPT position capacity");
+    }
+    void build_prefix(const float* cond_host, uint32_t n_cond, const float* speaker, const float* emotion, const uint32_t* text,
+                      uint32_t n_text, uint32_t language, float* out, uint32_t capacity_rows, uint32_t* rows) {
+        std::vector<uint32_t> ids;
+        prepare_tail(text, n_text, language, ids);
+        const uint32_t total = n_cond + static_cast<uint32_t>(ids.size()) + 1;
+        if (total > capacity_rows) throw std::invalid_argument("Prefix output buffer too small");
+        DevBuf<float> d;
+        d.alloc(static_cast<size_t>(total) * kWidth);
+        DevBuf<uint32_t> did;
+        did.alloc(ids.size());
+        HIP_CHECK(hipMemcpyAsync(did.p, ids.data(), ids.size() * 4, hipMemcpyHostToDevice, stream));
+        if (cond_host) {
+            HIP_CHECK(hipMemcpyAsync(d.p, cond_host, static_cast<size_t>(n_cond) * kWidth * 4, hipMemcpyHostToDevice, stream));
+        } else {
+            DevBuf<float> sp, em;
+            sp.alloc(192);
+            em.alloc(kWidth);
+            HIP_CHECK(hipMemcpyAsync(sp.p, speaker, 192 * 4, hipMemcpyHostToDevice, stream));
+            HIP_CHECK(hipMemcpyAsync(em.p, emotion, kWidth * 4, hipMemcpyHostToDevice, stream));
+            HIP_CHECK(hipMemsetAsync(d.p, 0, 3ull * kWidth * 4, stream));
+            HIP_CHECK(launch_speaker_row(spk_w.p, spk_b.p, sp.p, em.p, d.p, stream));
+            HIP_CHECK(hipStreamSynchronize(stream));
+        }
+        HIP_CHECK(launch_text_rows(text_emb.p, text_pos.p, lang_emb.p, mel_emb.p, mel_pos.p, did.p, static_cast<int>(ids.size()),
+                                   language, d.p + static_cast<size_t>(n_cond) * kWidth, stream));
+        HIP_CHECK(hipMemcpyAsync(out, d.p, d.n * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        *rows = total;
+    }
+
+    // ---------------------------------------------------------------- measurement
+    // Launches one decode kernel kind `iters` times (layer l = i % layers, so consecutive
+    // launches stream different weights) between two HIP events on the handle's stream.
+    void bench_kernel(int which, int batch, int iters, float* avg_ms, double* bytes) {
+        if (!layers || which < 0 || which > 5 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
+            throw std::invalid_argument("Invalid kernel benchmark request");
+        const int nb = gemv_batch_bucket(batch);
+        std::vector<SeqState> st(batch);
+        for (int b = 0; b < batch; ++b) {
+            itts_gen_options o;
+            itts_gen_options_default(&o);
+            st[b] = make_state(o, std::min<uint32_t>(cap - 2, 752), 2);
+            st[b].token = 1;
+            st[b].position = 2;
+        }
+        std::copy(st.begin(), st.end(), pinned_state);
+        upload_states(batch);
+        HIP_CHECK(hipStreamSynchronize(stream));
+        auto launch = [&](int l) {
+            const float* par = params.p + static_cast<size_t>(l) * kParLayer;
+            GemvArgs a = gemv_base(batch);
+            a.x_stride = kWidth;
+            a.out_stride = kWidth;
+            switch (which) {
+                case 0:
+                    a.w = w_ptr(off_qkv[l]); a.bias = par + kParQkvB; a.rows = kQkv; a.x = h.p; a.ln_w = par + kParLn1W;
+                    a.ln_b = par + kParLn1B; a.q = q.p; a.kv_layer_off = kv_layer_off(l);
+                    HIP_CHECK(launch_gemv_qkv(a, nb, bf16, false, stream));
+                    break;
+                case 1:
+                    a.w = w_ptr(off_proj[l]); a.bias = par + kParProjB; a.rows = kWidth; a.x = attn.p; a.resid = h.p; a.out = hmid.p;
+                    HIP_CHECK(launch_gemv_proj(a, nb, bf16, stream));
+                    break;
+                case 2:
+                    a.w = w_ptr(off_fc[l]); a.bias = par + kParFcB; a.rows = kFfn; a.x = hmid.p; a.ln_w = par + kParLn2W;
+                    a.ln_b = par + kParLn2B; a.out = ff.p; a.out_stride = kFfn;
+                    HIP_CHECK(launch_gemv_fc(a, nb, bf16, stream));
+                    break;
+                case 3:
+                    a.w = w_ptr(off_fc2[l]); a.bias = par + kParFc2B; a.rows = kWidth; a.x = ff.p; a.x_stride = kFfn; a.resid = hmid.p;
+                    a.out = h.p;
+                    HIP_CHECK(launch_gemv_fc2(a, nb, bf16, stream));
+                    break;
+                case 4:
+                    enqueue_head(batch, nb);
+                    break;
+                default: {
+                    AttnArgs t{};
+                    t.q = q.p; t.kv = kv.p; t.kv_slot_stride = kv_slot_stride; t.kv_layer_off = kv_layer_off(l); t.kv_v_off = kv_v_off;
+                    t.kv_cap = cap; t.partial = partial.p; t.ticket = ticket.p; t.out = attn.p; t.state = state.p; t.nseq = batch; t.splits = splits;
+                    HIP_CHECK(launch_attention(t, nb, stream));
+                }
+            }
+        };
+        for (int i = 0; i < std::min(iters, layers); ++i) launch(i % layers);  // warm-up
+        HIP_CHECK(hipEventRecord(ev[0], stream));
+        for (int i = 0; i < iters; ++i) launch(i % layers);
+        HIP_CHECK(hipEventRecord(ev[1], stream));
+        HIP_CHECK(hipEventSynchronize(ev[1]));
+        float ms = 0;
+        HIP_CHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        *avg_ms = ms / iters;
+        const double e = static_cast<double>(elt);
+        const double rows[5] = {kQkv, kWidth, kFfn, kWidth, kMelVocab};
+        const double cols[5] = {kWidth, kWidth, kWidth, kFfn, kWidth};
+        if (which < 5) {
+            // weights + bias + input rows (+ LayerNorm params) + outputs, per launch
+            *bytes = rows[which] * cols[which] * e + rows[which] * 4.0 + batch * cols[which] * 4.0 + batch * rows[which] * 4.0 +
+                     ((which == 0 || which == 2) ? 2.0 * kWidth * 4 : 0.0) + (which == 4 ? 4.0 * kWidth * 4 : 0.0) +
+                     ((which == 1 || which == 3) ? batch * rows[which] * 4.0 : 0.0);
+        } else {
+            *bytes = static_cast<double>(batch) * 2.0 * (st[0].n + 1) * kWidth * 4.0;  // K and V rows read
+        }
+    }
+
+    // ---------------------------------------------------------------- beams
+    void generate_beams(const float* prefix, uint32_t rows, const itts_gen_options& config, uint32_t maximum,
+                        std::vector<uint32_t>& result, bool& eos);
+};
+
+void Engine::generate(const float* prefix, uint32_t rows, const itts_gen_options& opt, uint32_t max_tokens, uint32_t* codes_out,
+                      uint32_t* n_codes, int32_t* stopped) {
+    itts_gen_options c = opt;
+    check_prefix(rows);
+    validate_generation(c, max_tokens, rows, mel_pos_rows, cap);
+    if (c.num_beams > 1) {
+        std::vector<uint32_t> out;
+        bool eos = false;
+        generate_beams(prefix, rows, c, max_tokens, out, eos);
+        std::copy(out.begin(), out.end(), codes_out);
+        *n_codes = static_cast<uint32_t>(out.size());
+        *stopped = eos ? 1 : 0;
+        return;
+    }
+    generate_batch({prefix}, {rows}, {c}, max_tokens, codes_out, n_codes, stopped);
+}
+
+void Engine::generate_beams(const float*, uint32_t, const itts_gen_options&, uint32_t, std::vector<uint32_t>&, bool&) {
+    throw std::runtime_error("Beam search is not available in this build");
+}
+
+}  // namespace itts
+
+// ==================================================================== C ABI
+
+struct itts_gpt {
+    itts::Engine e;
+};
+struct itts_gpt_state {
+    std::unique_ptr<itts::Snapshot> s;
+};
+
+namespace {
+template <class F>
+int guarded(itts_gpt* h, F&& f) {
+    try {
+        f();
+        return ITTS_OK;
+    } catch (const std::invalid_argument& e) {
+        if (h) h->e.last_error = e.what();
+        return ITTS_EINVAL;
+    } catch (const std::runtime_error& e) {
+        if (h) h->e.last_error = e.what();
+        return ITTS_ERUNTIME;
+    } catch (const std::exception& e) {
+        if (h) h->e.last_error = e.what();
+        return ITTS_ELOGIC;
+    }
+}
+}  // namespace
+
+extern "C" {
+
+void itts_gen_options_default(itts_gen_options* o) {
+    std::memset(o, 0, sizeof(*o));
+    o->do_sample = 1;
+    o->seed = 20261002ull;
+    o->temperature = 0.8f;
+    o->top_k = 30;
+    o->top_p = 0.8f;
+    o->repetition_penalty = 10.0f;
+    o->num_beams = 1;
+    o->length_penalty = 0.0f;
+}
+
+int itts_gpt_create(const itts_tensor* tensors, int32_t count, const itts_gpt_config* cfg, itts_gpt** out) {
+    if (!out) return ITTS_EINVAL;
+    *out = nullptr;
+    auto h = std::make_unique<itts_gpt>();
+    try {
+        h->e.create(tensors, count, cfg);
+    } catch (const std::invalid_argument& e) {
+        itts::g_create_error = e.what();
+        return ITTS_EINVAL;
+    } catch (const std::exception& e) {
+        itts::g_create_error = e.what();
+        return ITTS_ERUNTIME;
+    }
+    *out = h.release();
+    return ITTS_OK;
+}
+
+void itts_gpt_destroy(itts_gpt* h) { delete h; }
+
+const char* itts_gpt_last_error(const itts_gpt* h) { return h ? h->e.last_error.c_str() : itts::g_create_error.c_str(); }
+
+int itts_gpt_prepare(itts_gpt* h, const float* speaker, const float* emotion, const uint32_t* text, uint32_t n_text,
+                     uint32_t language, float* prefix_out, uint32_t capacity_rows, uint32_t* rows) {
+    return guarded(h, [&] {
+        if (!h->e.has_speaker || !speaker || !emotion) throw std::invalid_argument("Invalid GPT conditioning dimensions");
+        h->e.build_prefix(nullptr, 3, speaker, emotion, text, n_text, language, prefix_out, capacity_rows, rows);
+    });
+}
+
+int itts_gpt_prepare_cond(itts_gpt* h, const float* cond, uint32_t n_cond, const uint32_t* text, uint32_t n_text,
+                          uint32_t language, float* prefix_out, uint32_t capacity_rows, uint32_t* rows) {
+    return guarded(h, [&] {
+        if (!cond || !n_cond) throw std::invalid_argument("Invalid GPT conditioning dimensions");
+        h->e.build_prefix(cond, n_cond, nullptr, nullptr, text, n_text, language, prefix_out, capacity_rows, rows);
+    });
+}
+
+int itts_gpt_prefill(itts_gpt* h, const float* prefix, uint32_t rows, float* logits) {
+    return guarded(h, [&] { h->e.prefill(prefix, rows, logits); });
+}
+
+int itts_gpt_step(itts_gpt* h, uint32_t code, uint32_t position, float* logits) {
+    return guarded(h, [&] { h->e.step(code, position, logits); });
+}
+
+uint32_t itts_gpt_cached_tokens(const itts_gpt* h) { return h->e.cached; }
+
+int itts_gpt_checkpoint(itts_gpt* h, itts_gpt_state** out) {
+    return guarded(h, [&] {
+        auto s = std::make_unique<itts_gpt_state>();
+        s->s.reset(h->e.checkpoint());
+        *out = s.release();
+    });
+}
+
+int itts_gpt_restore(itts_gpt* h, const itts_gpt_state* state) {
+    return guarded(h, [&] {
+        if (!state || !state->s) throw std::invalid_argument("Invalid KV restore");
+        h->e.restore(*state->s);
+    });
+}
+
+uint32_t itts_gpt_state_tokens(const itts_gpt_state* state) { return state && state->s ? state->s->tokens : 0; }
+void itts_gpt_state_release(itts_gpt_state* state) { delete state; }
+
+int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options, uint32_t max_tokens,
+                      uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
+    return guarded(h, [&] { h->e.generate(prefix, rows, *options, max_tokens, codes_out, n_codes, stopped); });
+}
+
+int itts_gpt_generate_batch(itts_gpt* h, uint32_t batch, const float* const* prefixes, const uint32_t* rows,
+                            const itts_gen_options* options, uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes,
+                            int32_t* stopped) {
+    return guarded(h, [&] {
+        std::vector<const float*> p(prefixes, prefixes + batch);
+        std::vector<uint32_t> r(rows, rows + batch);
+        std::vector<itts_gen_options> o(options, options + batch);
+        h->e.generate_batch(p, r, o, max_tokens, codes_out, n_codes, stopped);
+    });
+}
+
+int itts_gpt_apply_processors(itts_gpt* h, const float* logits, uint32_t vocab, const uint32_t* history, uint32_t n_history,
+                              const itts_gen_options* options, float* out) {
+    return guarded(h, [&] { h->e.apply_processors(logits, vocab, history, n_history, *options, out); });
+}
+
+int itts_gpt_sample(itts_gpt* h, const float* processed, uint32_t vocab, uint64_t* rng_state, uint32_t draws, uint32_t* tokens) {
+    return guarded(h, [&] { h->e.sample(processed, vocab, rng_state, draws, tokens); });
+}
+
+int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t iters, float* avg_ms, double* bytes_per_launch) {
+    return guarded(h, [&] { h->e.bench_kernel(which, static_cast<int>(batch), static_cast<int>(iters), avg_ms, bytes_per_launch); });
+}
+
+int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out) {
+    if (!h || !out) return ITTS_EINVAL;
+    *out = h->e.timing;
+    return ITTS_OK;
+}
+
+void itts_synthetic_normal(float* out, size_t n, uint64_t seed, float mean, float stddev) {
+    auto mix = [](uint64_t z) {
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    };
+    const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < threads; ++t) {
+        pool.emplace_back([=] {
+            const size_t lo = n * t / threads, hi = n * (t + 1) / threads;
+            for (size_t i = lo; i < hi; ++i) {
+                // SplitMix64 outputs 2i and 2i+1 of the stream seeded with `seed`.
+                const uint64_t a = mix(seed + (2 * i + 1) * 0x9E3779B97F4A7C15ull);
+                const uint64_t b = mix(seed + (2 * i + 2) * 0x9E3779B97F4A7C15ull);
+                const double u1 = (static_cast<double>(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+                const double u2 = static_cast<double>(b >> 11) * (1.0 / 9007199254740992.0);
+                const double z = std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+                out[i] = static_cast<float>(mean + stddev * z);
+            }
+        });
+    }
+    for (auto& th : pool) th.join();
+}
+
+}  // extern "C"

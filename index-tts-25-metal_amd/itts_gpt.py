@@ -1,0 +1,403 @@
+"""Python binding of the MI355X-native IndexTTS 2.5 GPT semantic-token loop.
+
+Mirrors the reference's C++ interface (include/itts25/gpt.hpp:7-43):
+
+    GenerationOptions, GenerationResult, GptState, GptDecoder
+        .prepare(speaker, emotion, text, language)    gpt.cpp:42-71
+        .prefill(prefix)                              gpt.cpp:72-78
+        .step(code, position)                         gpt.cpp:79-85
+        .generate(prefix, options, max_tokens=1500)   gpt_sampling.cpp:168-245
+        .checkpoint() / .restore(state)               gpt.cpp:86-87
+        .cached_tokens()
+    apply_gpt_sampling_processors(logits, history, options)   gpt_sampling.cpp:28-128
+
+Everything runs through the C ABI of libitts_gpt.so (include/itts_gpt.h); there is
+no CPU path.  The reference's exception kinds map to InvalidArgument (a ValueError,
+std::invalid_argument), GptRuntimeError (a RuntimeError, std::runtime_error) and
+LogicError (std::logic_error), with the reference's messages.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import zlib
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libitts_gpt.so"
+
+WIDTH = 1280
+HEADS = 20
+FFN = 5120
+MEL_VOCAB = 8194
+MEL_START = 8192
+MEL_STOP = 8193
+
+
+class InvalidArgument(ValueError):
+    """std::invalid_argument in the reference."""
+
+
+class GptRuntimeError(RuntimeError):
+    """std::runtime_error in the reference."""
+
+
+class LogicError(Exception):
+    """std::logic_error in the reference."""
+
+
+class _Tensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("data", C.c_void_p), ("shape", C.c_int64 * 4), ("ndim", C.c_int32), ("_pad", C.c_int32)]
+
+
+class _Config(C.Structure):
+    _fields_ = [("kv_capacity", C.c_uint32), ("max_batch", C.c_uint32), ("weight_dtype", C.c_uint32), ("flags", C.c_uint32)]
+
+
+class _Options(C.Structure):
+    _fields_ = [
+        ("do_sample", C.c_int32), ("_pad0", C.c_uint32), ("seed", C.c_uint64), ("temperature", C.c_float),
+        ("top_k", C.c_uint32), ("top_p", C.c_float), ("repetition_penalty", C.c_float), ("num_beams", C.c_uint32),
+        ("length_penalty", C.c_float), ("suppress_stop", C.c_uint32), ("_pad1", C.c_uint32),
+    ]
+
+
+class _Timing(C.Structure):
+    _fields_ = [("prefill_ms", C.c_float), ("decode_ms", C.c_float), ("decode_steps", C.c_uint32), ("_pad", C.c_uint32)]
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(f"HIP extension not built: {LIB_PATH} is missing (run index-tts-25-metal_amd/build.py)")
+    lib = C.CDLL(str(LIB_PATH))
+    P = C.c_void_p
+    u32, i32, f32p, u32p = C.c_uint32, C.c_int32, C.POINTER(C.c_float), C.POINTER(C.c_uint32)
+    sig = {
+        "itts_gen_options_default": (None, [C.POINTER(_Options)]),
+        "itts_gpt_create": (C.c_int, [C.POINTER(_Tensor), i32, C.POINTER(_Config), C.POINTER(P)]),
+        "itts_gpt_destroy": (None, [P]),
+        "itts_gpt_last_error": (C.c_char_p, [P]),
+        "itts_gpt_prepare": (C.c_int, [P, f32p, f32p, u32p, u32, u32, f32p, u32, u32p]),
+        "itts_gpt_prepare_cond": (C.c_int, [P, f32p, u32, u32p, u32, u32, f32p, u32, u32p]),
+        "itts_gpt_prefill": (C.c_int, [P, f32p, u32, f32p]),
+        "itts_gpt_step": (C.c_int, [P, u32, u32, f32p]),
+        "itts_gpt_cached_tokens": (u32, [P]),
+        "itts_gpt_checkpoint": (C.c_int, [P, C.POINTER(P)]),
+        "itts_gpt_restore": (C.c_int, [P, P]),
+        "itts_gpt_state_tokens": (u32, [P]),
+        "itts_gpt_state_release": (None, [P]),
+        "itts_gpt_generate": (C.c_int, [P, f32p, u32, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
+        "itts_gpt_generate_batch": (C.c_int, [P, u32, C.POINTER(f32p), u32p, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
+        "itts_gpt_apply_processors": (C.c_int, [P, f32p, u32, u32p, u32, C.POINTER(_Options), f32p]),
+        "itts_gpt_sample": (C.c_int, [P, f32p, u32, C.POINTER(C.c_uint64), u32, u32p]),
+        "itts_gpt_last_timing": (C.c_int, [P, C.POINTER(_Timing)]),
+        "itts_gpt_bench_kernel": (C.c_int, [P, i32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
+        "itts_synthetic_normal": (None, [f32p, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = _load()
+
+
+def exported_symbols() -> List[str]:
+    """Names of the C ABI entry points bound here (all declared in include/itts_gpt.h)."""
+    return [n for n in dir(_lib) if n.startswith("itts_")]
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _up(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+@dataclass
+class GenerationOptions:
+    """itts25::GenerationOptions (gpt.hpp:7-16) plus suppress_stop (fixed-length runs)."""
+
+    do_sample: bool = True
+    seed: int = 20261002
+    temperature: float = 0.8
+    top_k: int = 30
+    top_p: float = 0.8
+    repetition_penalty: float = 10.0
+    num_beams: int = 1
+    length_penalty: float = 0.0
+    suppress_stop: bool = False
+
+    def _c(self) -> _Options:
+        return _Options(int(bool(self.do_sample)), 0, int(self.seed) & (2**64 - 1), float(self.temperature), int(self.top_k),
+                        float(self.top_p), float(self.repetition_penalty), int(self.num_beams), float(self.length_penalty),
+                        int(bool(self.suppress_stop)), 0)
+
+
+@dataclass
+class GenerationResult:
+    codes: List[int] = field(default_factory=list)
+    stopped: bool = False
+
+
+class GptState:
+    """Device snapshot of the cached KV rows (gpt.hpp:18)."""
+
+    def __init__(self, ptr: int):
+        self._ptr = C.c_void_p(ptr)
+        self.tokens = int(_lib.itts_gpt_state_tokens(self._ptr))
+
+    def __del__(self):
+        if getattr(self, "_ptr", None) and self._ptr.value:
+            _lib.itts_gpt_state_release(self._ptr)
+            self._ptr = C.c_void_p()
+
+
+def _raise(status: int, msg: str) -> None:
+    if status == -1:
+        raise InvalidArgument(msg)
+    if status == -2:
+        raise GptRuntimeError(msg)
+    raise LogicError(msg)
+
+
+class GptDecoder:
+    """itts25::GptDecoder on one MI355X (gpt.hpp:22-43)."""
+
+    def __init__(self, weights: Optional[Dict[str, np.ndarray]], kv_capacity: int = 4096, max_batch: int = 1,
+                 weight_dtype: str = "f32"):
+        self._h = C.c_void_p()
+        self._keep = []
+        tensors = []
+        for name, arr in (weights or {}).items():
+            a = np.ascontiguousarray(arr, dtype=np.float32)
+            self._keep.append(a)
+            shape = (C.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
+            tensors.append(_Tensor(name.encode(), a.ctypes.data, shape, a.ndim, 0))
+        arr_t = (_Tensor * max(1, len(tensors)))(*tensors)
+        cfg = _Config(int(kv_capacity), int(max_batch), 1 if weight_dtype == "bf16" else 0, 0)
+        st = _lib.itts_gpt_create(arr_t, len(tensors), C.byref(cfg), C.byref(self._h))
+        self._keep = []  # weights live on the device now
+        if st != 0:
+            _raise(st, _lib.itts_gpt_last_error(None).decode())
+        self.kv_capacity = int(kv_capacity)
+        self.max_batch = int(max_batch)
+
+    def close(self) -> None:
+        if self._h.value:
+            _lib.itts_gpt_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def _check(self, st: int) -> None:
+        if st != 0:
+            _raise(st, _lib.itts_gpt_last_error(self._h).decode())
+
+    # gpt.cpp:42-71
+    def prepare(self, speaker: np.ndarray, emotion: np.ndarray, text: Sequence[int], language: int) -> np.ndarray:
+        sp = np.ascontiguousarray(speaker, dtype=np.float32)
+        em = np.ascontiguousarray(emotion, dtype=np.float32)
+        if sp.size != 192 or em.size != WIDTH:
+            raise InvalidArgument("Invalid GPT conditioning dimensions")
+        ids = np.ascontiguousarray(np.asarray(text, dtype=np.uint32))
+        cap = 3 + len(ids) + 3
+        out = np.zeros((cap, WIDTH), np.float32)
+        rows = C.c_uint32()
+        self._check(_lib.itts_gpt_prepare(self._h, _fp(sp), _fp(em), _up(ids), len(ids), int(language), _fp(out), cap, C.byref(rows)))
+        return out[: rows.value].reshape(-1)
+
+    def prepare_cond(self, cond: np.ndarray, text: Sequence[int], language: int) -> np.ndarray:
+        """prepare() with the conditioning rows given directly (e.g. synthetic latents)."""
+        cd = np.ascontiguousarray(cond, dtype=np.float32).reshape(-1, WIDTH)
+        ids = np.ascontiguousarray(np.asarray(text, dtype=np.uint32))
+        cap = cd.shape[0] + len(ids) + 3
+        out = np.zeros((cap, WIDTH), np.float32)
+        rows = C.c_uint32()
+        self._check(_lib.itts_gpt_prepare_cond(self._h, _fp(cd), cd.shape[0], _up(ids), len(ids), int(language), _fp(out), cap,
+                                               C.byref(rows)))
+        return out[: rows.value].reshape(-1)
+
+    @staticmethod
+    def _prefix(prefix: np.ndarray) -> np.ndarray:
+        p = np.ascontiguousarray(prefix, dtype=np.float32).reshape(-1)
+        if p.size == 0 or p.size % WIDTH:
+            raise InvalidArgument("Invalid GPT prefill dimensions")
+        return p
+
+    def prefill(self, prefix: np.ndarray) -> np.ndarray:
+        p = self._prefix(prefix)
+        out = np.empty(MEL_VOCAB, np.float32)
+        self._check(_lib.itts_gpt_prefill(self._h, _fp(p), p.size // WIDTH, _fp(out)))
+        return out
+
+    def step(self, code: int, position: int) -> np.ndarray:
+        out = np.empty(MEL_VOCAB, np.float32)
+        self._check(_lib.itts_gpt_step(self._h, int(code) & 0xFFFFFFFF, int(position) & 0xFFFFFFFF, _fp(out)))
+        return out
+
+    def generate(self, prefix: np.ndarray, options: GenerationOptions, max_tokens: int = 1500) -> GenerationResult:
+        p = self._prefix(prefix)
+        codes = np.zeros(max(1, int(max_tokens)), np.uint32)
+        n = C.c_uint32()
+        stopped = C.c_int32()
+        o = options._c()
+        self._check(_lib.itts_gpt_generate(self._h, _fp(p), p.size // WIDTH, C.byref(o), int(max_tokens), _up(codes), C.byref(n),
+                                           C.byref(stopped)))
+        return GenerationResult([int(c) for c in codes[: n.value]], bool(stopped.value))
+
+    def generate_batch(self, prefixes: Sequence[np.ndarray], options, max_tokens: int) -> List[GenerationResult]:
+        ps = [self._prefix(p) for p in prefixes]
+        B = len(ps)
+        opts = list(options) if isinstance(options, (list, tuple)) else [options] * B
+        ptrs = (C.POINTER(C.c_float) * B)(*[_fp(p) for p in ps])
+        rows = np.array([p.size // WIDTH for p in ps], np.uint32)
+        copts = (_Options * B)(*[o._c() for o in opts])
+        codes = np.zeros((B, max(1, int(max_tokens))), np.uint32)
+        n = np.zeros(B, np.uint32)
+        stopped = np.zeros(B, np.int32)
+        self._check(_lib.itts_gpt_generate_batch(self._h, B, ptrs, _up(rows), copts, int(max_tokens), _up(codes), _up(n),
+                                                 stopped.ctypes.data_as(C.POINTER(C.c_int32))))
+        return [GenerationResult([int(c) for c in codes[b, : n[b]]], bool(stopped[b])) for b in range(B)]
+
+    def checkpoint(self) -> GptState:
+        ptr = C.c_void_p()
+        self._check(_lib.itts_gpt_checkpoint(self._h, C.byref(ptr)))
+        return GptState(ptr.value)
+
+    def restore(self, state: GptState) -> None:
+        self._check(_lib.itts_gpt_restore(self._h, state._ptr))
+
+    def cached_tokens(self) -> int:
+        return int(_lib.itts_gpt_cached_tokens(self._h))
+
+    def last_timing(self) -> dict:
+        t = _Timing()
+        self._check(_lib.itts_gpt_last_timing(self._h, C.byref(t)))
+        return {"prefill_ms": t.prefill_ms, "decode_ms": t.decode_ms, "decode_steps": t.decode_steps}
+
+    KERNELS = ("gemv_c_attn", "gemv_attn_proj", "gemv_c_fc", "gemv_mlp_proj", "gemv_mel_head", "attention")
+
+    def bench_kernel(self, which: str, iters: int = 240, batch: int = 1) -> dict:
+        """Mean duration (HIP events) and algorithmic bytes of one decode kernel kind."""
+        ms = C.c_float()
+        by = C.c_double()
+        self._check(_lib.itts_gpt_bench_kernel(self._h, self.KERNELS.index(which), int(batch), int(iters), C.byref(ms), C.byref(by)))
+        return {"avg_ms": float(ms.value), "bytes": float(by.value)}
+
+    # Processors / sampler on this handle's stream.
+    def apply_processors(self, logits: np.ndarray, history: Sequence[int], options: GenerationOptions) -> np.ndarray:
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        hist = np.ascontiguousarray(np.asarray(history, dtype=np.uint32))
+        out = np.empty_like(lg)
+        o = options._c()
+        self._check(_lib.itts_gpt_apply_processors(self._h, _fp(lg), lg.size, _up(hist), hist.size, C.byref(o), _fp(out)))
+        return out
+
+    def sample(self, processed: np.ndarray, rng_state: int, draws: int = 1):
+        pr = np.ascontiguousarray(processed, dtype=np.float32)
+        st = C.c_uint64(int(rng_state) & (2**64 - 1))
+        toks = np.zeros(int(draws), np.uint32)
+        self._check(_lib.itts_gpt_sample(self._h, _fp(pr), pr.size, C.byref(st), int(draws), _up(toks)))
+        return [int(t) for t in toks], int(st.value)
+
+
+_sampler_handle: Optional[GptDecoder] = None
+
+
+def _sampler() -> GptDecoder:
+    global _sampler_handle
+    if _sampler_handle is None:
+        _sampler_handle = GptDecoder(None)
+    return _sampler_handle
+
+
+def apply_gpt_sampling_processors(logits: np.ndarray, history: Sequence[int], options: GenerationOptions) -> np.ndarray:
+    """gpt_sampling.cpp:28-128, on the device (process-wide sampler-only handle)."""
+    return _sampler().apply_processors(logits, history, options)
+
+
+def sample_gpt_token(processed: np.ndarray, rng_state: int, draws: int = 1):
+    """gpt_sampling.cpp:130-165 `draws` times with SplitMix64 state rng_state; returns (tokens, new_state)."""
+    return _sampler().sample(processed, rng_state, draws)
+
+
+# ---------------------------------------------------------------------- synthetic inputs
+
+def synthetic_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    """Deterministic N(mean, std^2) values (Box-Muller over SplitMix64 keyed by (seed, index))."""
+    out = np.empty(int(n), np.float32)
+    _lib.itts_synthetic_normal(_fp(out), out.size, int(seed) & (2**64 - 1), float(mean), float(std))
+    return out
+
+
+def _tensor_seed(seed: int, name: str) -> int:
+    return (int(seed) * 0x9E3779B97F4A7C15 + zlib.crc32(name.encode())) & (2**64 - 1)
+
+
+def synthetic_weight_shapes(layers: int = 24, text_vocab: int = 12000, text_pos: int = 602, mel_pos: int = 1815,
+                            lang_vocab: int = 107, speaker: bool = True) -> Dict[str, tuple]:
+    """Tensor names and HF layouts of the IndexTTS 2.5 GPT (gpt.cpp:12-21)."""
+    s: Dict[str, tuple] = {}
+    if speaker:
+        s["gpt.spk_emb_proj.weight"] = (WIDTH, 192)
+        s["gpt.spk_emb_proj.bias"] = (WIDTH,)
+    s["gpt.text_embedding.weight"] = (text_vocab, WIDTH)
+    s["gpt.text_pos_embedding.emb.weight"] = (text_pos, WIDTH)
+    s["gpt.lang_embedding.weight"] = (lang_vocab, WIDTH)
+    s["gpt.mel_embedding.weight"] = (MEL_VOCAB, WIDTH)
+    s["gpt.mel_pos_embedding.emb.weight"] = (mel_pos, WIDTH)
+    for i in range(layers):
+        p = f"gpt.gpt.h.{i}"
+        s[p + ".ln_1.weight"] = (WIDTH,)
+        s[p + ".ln_1.bias"] = (WIDTH,)
+        s[p + ".attn.c_attn.weight"] = (WIDTH, 3 * WIDTH)
+        s[p + ".attn.c_attn.bias"] = (3 * WIDTH,)
+        s[p + ".attn.c_proj.weight"] = (WIDTH, WIDTH)
+        s[p + ".attn.c_proj.bias"] = (WIDTH,)
+        s[p + ".ln_2.weight"] = (WIDTH,)
+        s[p + ".ln_2.bias"] = (WIDTH,)
+        s[p + ".mlp.c_fc.weight"] = (WIDTH, FFN)
+        s[p + ".mlp.c_fc.bias"] = (FFN,)
+        s[p + ".mlp.c_proj.weight"] = (FFN, WIDTH)
+        s[p + ".mlp.c_proj.bias"] = (WIDTH,)
+    s["gpt.gpt.ln_f.weight"] = (WIDTH,)
+    s["gpt.gpt.ln_f.bias"] = (WIDTH,)
+    s["gpt.final_norm.weight"] = (WIDTH,)
+    s["gpt.final_norm.bias"] = (WIDTH,)
+    s["gpt.mel_head.weight"] = (MEL_VOCAB, WIDTH)
+    s["gpt.mel_head.bias"] = (MEL_VOCAB,)
+    return s
+
+
+def make_synthetic_weights(layers: int = 24, seed: int = 0, std: float = 0.02, ln_random: bool = False,
+                           **shape_kw) -> Dict[str, np.ndarray]:
+    """Random-init FP32 weights N(0, std^2); LayerNorm gamma=1, beta=0 unless ln_random."""
+    out: Dict[str, np.ndarray] = {}
+    for name, shape in synthetic_weight_shapes(layers, **shape_kw).items():
+        n = int(np.prod(shape))
+        is_ln = (".ln_" in name or "ln_f" in name or "final_norm" in name)
+        if is_ln and not ln_random:
+            out[name] = np.ones(shape, np.float32) if name.endswith("weight") else np.zeros(shape, np.float32)
+        elif is_ln:
+            mean = 1.0 if name.endswith("weight") else 0.0
+            out[name] = synthetic_normal(n, _tensor_seed(seed, name), mean, 0.1).reshape(shape)
+        else:
+            out[name] = synthetic_normal(n, _tensor_seed(seed, name), 0.0, std).reshape(shape)
+    return out
+
+
+def synthetic_prefix_inputs(n_text: int, seed: int, n_cond: int = 32, text_vocab: int = 12000):
+    """32 conditioning latents ~N(0,1)*0.5 and n_text ids uniform in [0, text_vocab)."""
+    cond = synthetic_normal(n_cond * WIDTH, _tensor_seed(seed, "cond"), 0.0, 0.5).reshape(n_cond, WIDTH)
+    rng = np.random.default_rng(seed)
+    text = rng.integers(0, text_vocab, size=n_text, dtype=np.int64).astype(np.uint32)
+    return cond, text

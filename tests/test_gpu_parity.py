@@ -1,0 +1,238 @@
+"""HIP path vs the CPU oracle and the reference-sampler fixtures (MI355X).
+
+Tolerances (north star): teacher-forced logits max-abs <= 1e-3 and relative (L2) <= 1e-4;
+greedy codes exact; processors (mask and values) and sampled tokens bit-exact given the
+same logits and RNG state.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden" / "sampling_golden.npz"
+LOGIT_ABS = 1e-3
+LOGIT_REL = 1e-4
+
+
+def assert_logits_close(got, ref, what=""):
+    err = float(np.max(np.abs(got - ref)))
+    rel = rel_err(got, ref)
+    assert err <= LOGIT_ABS and rel <= LOGIT_REL, f"{what}: max-abs {err:.3e} rel {rel:.3e}"
+    assert int(np.argmax(got)) == int(np.argmax(ref)), what
+
+
+# ---------------------------------------------------------------------------- sampler
+
+def _opts(itts, cfg):
+    return itts.GenerationOptions(temperature=float(cfg[0]), top_k=int(cfg[1]), top_p=float(cfg[2]),
+                                  repetition_penalty=float(cfg[3]), num_beams=int(cfg[4]))
+
+
+def test_processors_match_reference_golden(itts):
+    g = np.load(GOLDEN, allow_pickle=False)
+    cases = [k[: -len(".config")] for k in g.files if k.endswith(".config")]
+    assert cases
+    for case in cases:
+        out = itts.apply_gpt_sampling_processors(g[case + ".logits"], g[case + ".history"], _opts(itts, g[case + ".config"]))
+        assert np.array_equal(np.isfinite(out), g[case + ".allowed"].astype(bool)), case
+        assert np.array_equal(out, g[case + ".values"]), case
+
+
+def test_sampler_draws_match_reference_golden(itts):
+    g = np.load(GOLDEN, allow_pickle=False)
+    for case in [k[: -len(".draw_seed")] for k in g.files if k.endswith(".draw_seed")]:
+        toks, state = itts.sample_gpt_token(g[case + ".values"], int(g[case + ".draw_seed"][0]), len(g[case + ".draws"]))
+        assert toks == [int(t) for t in g[case + ".draws"]], case
+        assert state == int(g[case + ".draw_state"][0]), case
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_processors_and_draws_match_oracle_random(itts, oracle, seed):
+    rng = np.random.default_rng(seed)
+    configs = [(0.8, 30, 0.8, 10.0, 1), (1.0, 0, 0.5, 1.0, 1), (0.7, 1, 0.9, 2.0, 3), (1.3, 700, 0.95, 1.0, 2),
+               (1.0, 0, 1.0, 1.0, 1), (0.5, 30, 0.01, 10.0, 3), (1.0, 8193, 0.3, 1.5, 1), (0.9, 1500, 1.0, 3.0, 1)]
+    for logits in ((rng.standard_normal(8194) * 3).astype(np.float32),
+                   (np.round(rng.standard_normal(8194) * 3) / 3).astype(np.float32)):
+        hist = [1, 8192] + [int(x) for x in rng.integers(0, 8194, 30)]
+        for T, k, p, pen, beams in configs:
+            o = itts.GenerationOptions(temperature=T, top_k=k, top_p=p, repetition_penalty=pen, num_beams=beams)
+            got = itts.apply_gpt_sampling_processors(logits, hist, o)
+            exp = oracle.processors(logits, hist, oracle.options_from(o))
+            assert np.array_equal(got, exp), (T, k, p, pen, beams)
+            s = int(rng.integers(0, 2**63))
+            assert itts.sample_gpt_token(got, s, 8) == oracle.sample(got, s, 8)
+
+
+def test_processor_errors(itts):
+    lg = np.zeros(8194, np.float32)
+    with pytest.raises(itts.GptRuntimeError, match="temperature must be positive"):
+        itts.apply_gpt_sampling_processors(lg, [], itts.GenerationOptions(temperature=0.0))
+    with pytest.raises(itts.GptRuntimeError, match="repetition penalty must be positive"):
+        itts.apply_gpt_sampling_processors(lg, [], itts.GenerationOptions(repetition_penalty=-1.0))
+    with pytest.raises(itts.GptRuntimeError, match="received no finite logits"):
+        itts.sample_gpt_token(np.full(8194, -np.inf, np.float32), 1)
+
+
+# ---------------------------------------------------------------------------- small model (2 layers, real widths)
+
+@pytest.fixture(scope="module")
+def small(itts, oracle, small_weights):
+    dec = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=4)
+    orc = oracle.OracleGpt(small_weights, kv_capacity=1024)
+    cond, text = itts.synthetic_prefix_inputs(40, seed=1)
+    return dec, orc, cond, text
+
+
+def test_prepare_matches_oracle(small, itts):
+    dec, orc, cond, text = small
+    a = dec.prepare_cond(cond, text, 5)
+    b = orc.prepare_cond(cond, text, 5)
+    assert np.array_equal(a, b)
+    sp = itts.synthetic_normal(192, 3)
+    em = itts.synthetic_normal(1280, 4)
+    pa = dec.prepare(sp, em, text, 5)
+    pb = orc.prepare(sp, em, text, 5)
+    assert pa.shape == pb.shape
+    assert np.max(np.abs(pa - pb)) < 1e-5
+
+
+def test_prefill_and_steps_small(small):
+    dec, orc, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    assert_logits_close(dec.prefill(prefix), orc.prefill(prefix), "prefill")
+    assert dec.cached_tokens() == orc.cached_tokens() == prefix.size // 1280
+    for i, code in enumerate([17, 4000, 8191, 2]):
+        assert_logits_close(dec.step(code, i + 2), orc.step(code, i + 2), f"step {i}")
+    assert dec.cached_tokens() == orc.cached_tokens()
+
+
+def test_step_errors(small, itts):
+    dec, orc, cond, text = small
+    dec.prefill(dec.prepare_cond(cond, text, 0))
+    with pytest.raises(itts.InvalidArgument, match="valid cache, code and position"):
+        dec.step(8194, 2)
+    with pytest.raises(itts.InvalidArgument, match="valid cache, code and position"):
+        dec.step(3, 1815)
+    with pytest.raises(itts.InvalidArgument, match="Invalid GPT prefill dimensions"):
+        dec.prefill(np.zeros(1280 * 1025, np.float32))
+
+
+def test_checkpoint_restore(small):
+    dec, _, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    dec.prefill(prefix)
+    dec.step(10, 2)
+    st = dec.checkpoint()
+    assert st.tokens == dec.cached_tokens()
+    a = dec.step(11, 3)
+    dec.step(12, 4)
+    dec.restore(st)
+    assert dec.cached_tokens() == st.tokens
+    b = dec.step(11, 3)
+    assert np.array_equal(a, b)
+
+
+def test_step_is_deterministic(small):
+    dec, _, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    runs = []
+    for _ in range(2):
+        dec.prefill(prefix)
+        runs.append(dec.step(99, 2))
+    assert np.array_equal(runs[0], runs[1])
+
+
+def test_greedy_generate_small(small, itts, oracle):
+    dec, orc, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(do_sample=False, repetition_penalty=1.0)
+    r = dec.generate(prefix, o, 48)
+    codes, stopped = orc.generate(prefix, oracle.options_from(o), 48)
+    assert r.codes == codes and r.stopped == stopped
+    assert dec.cached_tokens() == orc.cached_tokens()
+
+
+def test_sampled_generate_small(small, itts, oracle):
+    dec, orc, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(do_sample=True, seed=42, temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=10.0)
+    r = dec.generate(prefix, o, 64)
+    codes, stopped = orc.generate(prefix, oracle.options_from(o), 64)
+    assert r.codes == codes and r.stopped == stopped
+
+
+def test_batch_generate_matches_single_and_oracle(small, itts, oracle):
+    dec, orc, cond, _ = small
+    rng = np.random.default_rng(7)
+    prefixes, opts = [], []
+    for b in range(3):
+        t = rng.integers(0, 12000, int(rng.integers(24, 60))).astype(np.uint32)
+        prefixes.append(dec.prepare_cond(cond, t, 0))
+        opts.append(itts.GenerationOptions(seed=100 + b, suppress_stop=True))
+    batch = dec.generate_batch(prefixes, opts, 40)
+    for b in range(3):
+        single = dec.generate(prefixes[b], opts[b], 40)
+        assert batch[b].codes == single.codes and batch[b].stopped == single.stopped
+        codes, stopped = orc.generate(prefixes[b], oracle.options_from(opts[b]), 40)
+        assert batch[b].codes == codes
+
+
+def test_generate_argument_errors(small, itts):
+    dec, _, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    with pytest.raises(itts.InvalidArgument, match="capacity exceeded"):
+        dec.generate(prefix, itts.GenerationOptions(), 1814)
+    with pytest.raises(itts.InvalidArgument, match="Invalid GPT generation parameters"):
+        dec.generate(prefix, itts.GenerationOptions(top_p=0.0), 8)
+    with pytest.raises(itts.InvalidArgument, match="Invalid beam search configuration"):
+        dec.generate(prefix, itts.GenerationOptions(num_beams=0), 8)
+
+
+def test_bf16_weights_logit_tolerance(small_weights, small, itts):
+    """BF16-stored weights, FP32 accumulate: logits within 5e-2 max-abs of the FP32 path."""
+    dec, _, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    ref = dec.prefill(prefix)
+    d16 = itts.GptDecoder(small_weights, kv_capacity=1024, weight_dtype="bf16")
+    got = d16.prefill(prefix)
+    assert float(np.max(np.abs(got - ref))) < 5e-2
+    s16 = d16.step(5, 2)
+    s32 = dec.step(5, 2)
+    assert float(np.max(np.abs(s16 - s32))) < 5e-2
+    d16.close()
+
+
+# ---------------------------------------------------------------------------- full model, config 1
+
+@pytest.fixture(scope="module")
+def full(itts, oracle, full_weights):
+    dec = itts.GptDecoder(full_weights, kv_capacity=4096)
+    orc = oracle.OracleGpt(full_weights, kv_capacity=4096)
+    cond, text = itts.synthetic_prefix_inputs(48, seed=0)
+    prefix = orc.prepare_cond(cond, text, 0)
+    return dec, orc, prefix
+
+
+def test_full_teacher_forced_logits(full):
+    dec, orc, prefix = full
+    assert prefix.size // 1280 == 83
+    assert_logits_close(dec.prefill(prefix), orc.prefill(prefix), "prefill")
+    for i, code in enumerate([100, 2000, 3000, 8000]):
+        assert_logits_close(dec.step(code, i + 2), orc.step(code, i + 2), f"decode.{i + 1}")
+
+
+def test_full_greedy_128(full, itts, oracle):
+    dec, orc, prefix = full
+    o = itts.GenerationOptions(do_sample=False, repetition_penalty=1.0)
+    try:
+        r = dec.generate(prefix, o, 128)
+        got = (r.codes, r.stopped)
+    except itts.GptRuntimeError as e:
+        got = str(e)
+    try:
+        exp = orc.generate(prefix, oracle.options_from(o), 128)
+    except oracle.OracleError as e:
+        exp = str(e)
+    assert got == exp

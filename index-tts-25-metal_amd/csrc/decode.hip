@@ -18,14 +18,20 @@
 //     of one head, 16 lanes per row (one float4 of the 64-dim row each), loads all K
 //     and V float4s up front, forms scores (q.k)*rsqrt(64), a max-subtracted exp and a
 //     partial sum of weights and weighted V;
-//   * the last workgroup of a head (atomic ticket) merges the splits with the usual
-//     rescaling exp(m_s - M) and writes out = sum(w v) / sum(w), then re-arms the ticket.
+//   * a second small kernel merges the splits of each head with the usual rescaling
+//     exp(m_s - M) and writes out = sum(w v) / sum(w); the kernel boundary orders the
+//     two passes, so no workgroup needs a device-scope fence or atomic.
 #include "kernels.h"
 
 namespace itts {
 namespace {
 
 constexpr int kNW = 4;  // waves per GEMV workgroup
+
+// Splits actually used for L keys: about kAttnSplitRows rows each, at most `max_splits`.
+__device__ __forceinline__ int live_splits(int L, int max_splits) {
+    return min(max_splits, max(1, (L + kAttnSplitRows - 1) / kAttnSplitRows));
+}
 
 template <int COLS, int RPW, int B, typename WT, int PRO, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
@@ -185,8 +191,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     if (b >= a.nseq) return;
     const SeqState& st = a.state[b];
     if (!st.active) return;
-    const int S = a.splits;
     const int L = static_cast<int>(st.n) + 1;  // cached rows + the row appended by this step
+    const int S = live_splits(L, a.splits);
+    if (s >= S) return;
     const int chunk = (L + S - 1) / S;
     const int p0 = s * chunk;
     const int p1 = min(L, p0 + chunk);
@@ -227,7 +234,6 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
     __shared__ float redm[4], reds[4];
     __shared__ float accs[16][kHeadDim + 4];
-    __shared__ int last;
     const float wm = wave_max(mloc);
     if (lane == 0) redm[wave] = wm;
     __syncthreads();
@@ -251,7 +257,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     accs[g][sub * 4 + 2] = acc.z;
     accs[g][sub * 4 + 3] = acc.w;
     __syncthreads();
-    float* part = a.partial + (static_cast<size_t>(b * kHeads + h) * S + s) * 68;
+    float* part = a.partial + (static_cast<size_t>(b * kHeads + h) * a.splits + s) * 68;
     if (t < kHeadDim) {
         float tot = 0.0f;
 #pragma unroll
@@ -262,26 +268,47 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             part[1] = ((reds[0] + reds[1]) + reds[2]) + reds[3];
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (t == 0) last = atomicAdd(&a.ticket[b * kHeads + h], 1u) == static_cast<unsigned>(S - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    if (t < kHeadDim) {
-        const float* pb = a.partial + static_cast<size_t>(b * kHeads + h) * S * 68;
-        float mg = -INFINITY;
-        for (int k = 0; k < S; ++k) mg = fmaxf(mg, __builtin_nontemporal_load(pb + k * 68));
-        float den = 0.0f, num = 0.0f;
-        for (int k = 0; k < S; ++k) {
-            const float ms = __builtin_nontemporal_load(pb + k * 68);
-            const float wgt = ms == -INFINITY ? 0.0f : expf(ms - mg);
-            den = __builtin_fmaf(__builtin_nontemporal_load(pb + k * 68 + 1), wgt, den);
-            num = __builtin_fmaf(__builtin_nontemporal_load(pb + k * 68 + 4 + t), wgt, num);
-        }
-        a.out[b * kWidth + h * kHeadDim + t] = num / den;
+}
+
+// Merge of the splits of one (sequence, head): out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// Wave w takes splits w, w+4, ...; every load is issued before the first use.
+__global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (b >= a.nseq || !a.state[b].active) return;
+    const int S = live_splits(static_cast<int>(a.state[b].n) + 1, a.splits);
+    const float* pb = a.partial + static_cast<size_t>(b * kHeads + h) * a.splits * 68;
+    constexpr int PW = kAttnMaxSplits / 4;
+    float mk[PW], lk[PW], ak[PW];
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const int k = wave + 4 * i;
+        const bool ok = k < S;
+        mk[i] = ok ? pb[k * 68] : -INFINITY;
+        lk[i] = ok ? pb[k * 68 + 1] : 0.0f;
+        ak[i] = ok ? pb[k * 68 + 4 + lane] : 0.0f;
     }
-    if (t == 0) atomicExch(&a.ticket[b * kHeads + h], 0u);
+    __shared__ float wm[4], wden[4], wnum[4][kHeadDim];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) m = fmaxf(m, mk[i]);
+    if (lane == 0) wm[wave] = m;
+    __syncthreads();
+    const float mg = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float den = 0.0f, num = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const float wgt = mk[i] == -INFINITY ? 0.0f : expf(mk[i] - mg);
+        den = __builtin_fmaf(lk[i], wgt, den);
+        num = __builtin_fmaf(ak[i], wgt, num);
+    }
+    wnum[wave][lane] = num;
+    if (lane == 0) wden[wave] = den;
+    __syncthreads();
+    if (wave == 0) {
+        const float d = ((wden[0] + wden[1]) + wden[2]) + wden[3];
+        const float n = ((wnum[0][lane] + wnum[1][lane]) + wnum[2][lane]) + wnum[3][lane];
+        a.out[b * kWidth + h * kHeadDim + lane] = n / d;
+    }
 }
 
 }  // namespace
@@ -312,6 +339,7 @@ hipError_t launch_gemv_head(const GemvArgs& a, int batch, bool bf16, hipStream_t
 
 hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
     hipLaunchKernelGGL(attention_kernel, dim3(a.splits, kHeads, batch), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(kHeads, batch), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -68,14 +68,16 @@ struct AttnArgs {
     size_t kv_v_off;
     uint32_t kv_cap;
     const uint8_t* table;   // beam row-owner table [batch][kv_cap] (slot holding each row) or null
-    float* partial;         // [batch][20][splits][68]
-    uint32_t* ticket;       // [batch][20], zero between launches
+    float* partial;         // [batch][20][splits][68]: m, l, -, -, acc[64]
     float* out;             // [batch][1280]
     const SeqState* state;
     int nseq;               // sequences with state entries; slots >= nseq are padding
     int splits;
 };
-constexpr int kAttnMaxChunk = 128;  // rows per split
+constexpr int kAttnMaxChunk = 128;   // rows per split at most
+constexpr int kAttnSplitRows = 64;   // target rows per split
+constexpr int kAttnMaxSplits = 64;   // splits per (sequence, head) at most
+// Split pass (grid splits x 20 x batch) then merge pass (grid 20 x batch).
 hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 
 // ------------------------------------------------------------------ sampler

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -102,7 +103,7 @@ struct Engine {
     DevBuf<float> kv;
     size_t kv_slot_stride = 0, kv_layer_stride = 0, kv_v_off = 0;
     DevBuf<float> h, hmid, q, attn, ff, logits, partial;
-    DevBuf<uint32_t> ticket, codes, status, d_parent;
+    DevBuf<uint32_t> codes, status, d_parent;
     DevBuf<SeqState> state;  // kMaxBatch + 1 entries; the last one serves the processor/sampler API
     DevBuf<uint8_t> seen, seen_tmp, table, table_tmp;
     DevBuf<double> probs;
@@ -115,6 +116,7 @@ struct Engine {
     uint32_t* pinned = nullptr;  // host pinned staging (flags)
     SeqState* pinned_state = nullptr;
     int splits = 16;
+    bool use_graphs = true;  // ITTS_GPT_GRAPHS=0: launch the same kernels eagerly (profilers)
     std::map<std::tuple<int, int, bool, bool>, hipGraphExec_t> graphs;
     hipEvent_t ev[4] = {};
     uint32_t cached = 0;
@@ -153,6 +155,7 @@ struct Engine {
     }
 
     void create(const itts_tensor* tensors, int32_t count, const itts_gpt_config* cfg) {
+        if (const char* g = std::getenv("ITTS_GPT_GRAPHS")) use_graphs = std::strcmp(g, "0") != 0;
         init_common();
         if (count == 0) return;  // sampler-only handle
         std::unordered_map<std::string, HostTensor> by;
@@ -277,10 +280,11 @@ struct Engine {
         q.alloc(B * kWidth);
         attn.alloc(B * kWidth);
         ff.alloc(B * kFfn);
-        splits = std::max<int>(16, (cap + kAttnMaxChunk - 1) / kAttnMaxChunk);
+        // Enough splits that no split exceeds kAttnMaxChunk rows at full capacity.
+        splits = std::max<int>((cap + kAttnSplitRows - 1) / kAttnSplitRows, (cap + kAttnMaxChunk - 1) / kAttnMaxChunk);
+        splits = std::min(splits, kAttnMaxSplits);
+        if (static_cast<uint32_t>(splits) * kAttnMaxChunk < cap) throw std::invalid_argument("KV capacity exceeds attention splits");
         partial.alloc(B * kHeads * splits * 68);
-        ticket.alloc(B * kHeads);
-        HIP_CHECK(hipMemsetAsync(ticket.p, 0, ticket.n * 4, stream));
         codes.alloc((B + 1) * cap);
         d_parent.alloc(B);
         seen_tmp.alloc((B + 1) * kMelVocab);
@@ -329,8 +333,7 @@ struct Engine {
             t.kv_cap = cap;
             t.table = use_table ? table.p : nullptr;
             t.partial = partial.p;
-            t.ticket = ticket.p;
-            t.out = attn.p;
+                        t.out = attn.p;
             t.state = state.p;
             t.nseq = nseq;
             t.splits = splits;
@@ -401,6 +404,16 @@ struct Engine {
         s.status = status.p;
         s.mode = mode;
         return s;
+    }
+
+    // Runs one step (forward [+ sampler]) as a replay of its captured graph, or eagerly.
+    void run_step(int nseq, int nb, bool sampler, bool use_table) {
+        if (use_graphs) {
+            HIP_CHECK(hipGraphLaunch(graph(nseq, nb, sampler, use_table), stream));
+            return;
+        }
+        enqueue_forward(nseq, nb, use_table);
+        if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
     }
 
     hipGraphExec_t graph(int nseq, int nb, bool sampler, bool use_table) {
@@ -573,7 +586,7 @@ struct Engine {
         s.position = position;
         pinned_state[0] = s;
         upload_states(1);
-        HIP_CHECK(hipGraphLaunch(graph(1, 1, false, false), stream));
+        run_step(1, 1, false, false);
         HIP_CHECK(hipMemcpyAsync(out_logits, logits.p, kMelVocab * 4, hipMemcpyDeviceToHost, stream));
         HIP_CHECK(hipStreamSynchronize(stream));
         cached++;
@@ -609,14 +622,14 @@ struct Engine {
     // are in logits[0..nseq): sampler, then (forward + sampler) graph replays.
     void decode_loop(int nseq, uint32_t max_tokens) {
         const int nb = gemv_batch_bucket(nseq);
-        const hipGraphExec_t g = graph(nseq, nb, true, false);  // captured before any work is queued
+        if (use_graphs) (void)graph(nseq, nb, true, false);  // captured before any work is queued
         HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
         constexpr uint32_t kChunk = 16;
         uint32_t launched = 0;
         int k = 0;
         while (launched + 1 < max_tokens) {
             const uint32_t n = std::min(kChunk, max_tokens - 1 - launched);
-            for (uint32_t i = 0; i < n; ++i) HIP_CHECK(hipGraphLaunch(g, stream));
+            for (uint32_t i = 0; i < n; ++i) run_step(nseq, nb, true, false);
             launched += n;
             HIP_CHECK(hipMemcpyAsync(pinned + 16 * (k & 1), &state.p[0].active, 4, hipMemcpyDeviceToHost, stream));
             for (int b = 1; b < nseq; ++b)
@@ -848,7 +861,7 @@ struct Engine {
                 default: {
                     AttnArgs t{};
                     t.q = q.p; t.kv = kv.p; t.kv_slot_stride = kv_slot_stride; t.kv_layer_off = kv_layer_off(l); t.kv_v_off = kv_v_off;
-                    t.kv_cap = cap; t.partial = partial.p; t.ticket = ticket.p; t.out = attn.p; t.state = state.p; t.nseq = batch; t.splits = splits;
+                    t.kv_cap = cap; t.partial = partial.p; t.out = attn.p; t.state = state.p; t.nseq = batch; t.splits = splits;
                     HIP_CHECK(launch_attention(t, nb, stream));
                 }
             }

@@ -1,0 +1,279 @@
+// Beam-search scoring and candidate selection (src/gpt_sampling.cpp:190-245) on the device.
+//
+// beam_scores_kernel, one 1024-thread workgroup per parent beam:
+//   log_probs = logits - (peak + log(sum_i exp(logit_i - peak)))   (:207-210, float; the
+//   sum is formed by one thread in index order, exp/log evaluated in double and rounded,
+//   i.e. correctly rounded except on double-rounding ties), then the processors with the
+//   parent's repetition set (:211-212), then + the parent's beam score (:213).
+// beam_select_kernel, one workgroup:
+//   greedy: the take = 2*beams best of all parents' scores by (score desc, index asc)
+//   (std::partial_sort with index ties, :223-227); sampled: take draws without
+//   replacement with sample_gpt_token_from_logits (:217-222); then a stable sort of the
+//   candidates by score (:228).
+// The host reads the candidates and runs the reference's child/finish bookkeeping.
+#include "sampler_dev.h"
+
+namespace itts {
+namespace {
+using namespace sampling;
+
+__device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+__device__ __forceinline__ float logf_cr(float x) { return static_cast<float>(log(static_cast<double>(x))); }
+
+__global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
+    __shared__ Smem sm;
+    __shared__ float wred[NWAVE];
+    __shared__ float log_sum_s;
+    const int p = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float* lg = a.logits + static_cast<size_t>(p) * V;
+    float* e = reinterpret_cast<float*>(sm.sortbuf) + V;  // after s[] inside the union
+    float mloc = -INFINITY;
+    for (int i = t; i < V; i += NT) {
+        float v = lg[i];
+        if (a.suppress_stop && (i == kMelStart || i == kMelStop)) v = -INFINITY;
+        sm.s[i] = v;
+        mloc = fmaxf(mloc, v);
+    }
+    mloc = wave_max(mloc);
+    if (lane == 0) wred[wave] = mloc;
+    __syncthreads();
+    float peak = wred[0];
+    for (int w = 1; w < NWAVE; ++w) peak = fmaxf(peak, wred[w]);
+    for (int i = t; i < V; i += NT) e[i] = expf_cr(sm.s[i] - peak);
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < V; ++i) sum += e[i];
+        log_sum_s = peak + logf_cr(sum);
+    }
+    __syncthreads();
+    const float log_sum = log_sum_s;
+    for (int i = t; i < V; i += NT) sm.s[i] = sm.s[i] - log_sum;
+    __syncthreads();
+    bool topp = false;
+    const uint32_t st = run_processors(sm, a.seen + static_cast<size_t>(p) * V, a.penalty, a.temperature, a.top_k, a.top_p,
+                                       a.num_beams, a.probs + static_cast<size_t>(p) * V, true, &topp);
+    if (t == 0) a.status[1 + p] = st;
+    if (st != kOk) return;
+    const float score = a.beam_score[p];
+    float* out = a.all_scores + static_cast<size_t>(p) * V;
+    for (int i = t; i < V; i += NT) out[i] = sm.s[i] + score;
+}
+
+// kk-th largest (1-based) of src[0..n) in global memory.
+__device__ float radix_kth_largest_global(const float* src, int n, uint32_t kk, uint32_t* hist, uint32_t* sel) {
+    const int t = threadIdx.x, lane = t & 63;
+    uint32_t prefix = 0, mask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (t < 256) hist[t] = 0;
+        __syncthreads();
+        for (int i = t; i < n; i += NT) {
+            const uint32_t k = float_key(src[i]);
+            if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (t < 64) {
+            uint32_t c[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) c[q] = hist[255 - 4 * lane - q];
+            const uint32_t loc = c[0] + c[1] + c[2] + c[3];
+            uint32_t inc = loc;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += v;
+            }
+            const uint32_t exc = inc - loc;
+            if (exc < kk && kk <= inc) {
+                uint32_t run = exc;
+                int d = -1;
+                uint32_t above = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (d < 0) {
+                        if (run + c[q] >= kk) {
+                            d = 255 - 4 * lane - q;
+                            above = run;
+                        } else {
+                            run += c[q];
+                        }
+                    }
+                sel[0] = static_cast<uint32_t>(d);
+                sel[1] = above;
+            }
+        }
+        __syncthreads();
+        prefix |= sel[0] << shift;
+        mask |= 0xffu << shift;
+        kk -= sel[1];
+        __syncthreads();
+    }
+    return key_float(prefix);
+}
+
+// Block-wide exclusive scan of one count per thread; returns the thread's offset, *total the sum.
+__device__ uint32_t block_scan(uint32_t c, uint32_t* wtot, uint32_t* total) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    uint32_t inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+    }
+    if (lane == 63) wtot[wave] = inc;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+    for (int w = 0; w < NWAVE; ++w) {
+        if (w < wave) off += wtot[w];
+        tot += wtot[w];
+    }
+    __syncthreads();
+    *total = tot;
+    return off + inc - c;
+}
+
+__global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
+    __shared__ uint32_t hist[256], sel[2], wtot[NWAVE];
+    __shared__ uint32_t ids[2 * kMaxBeamTake];
+    __shared__ float wmax[NWAVE];
+    __shared__ float mx_s;
+    __shared__ uint32_t stop_s;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n = a.parents * V;
+    const float* S = a.all_scores;
+    const int take = a.take;
+    const int chunk = (n + NT - 1) / NT;
+    const int i0 = min(n, t * chunk), i1 = min(n, i0 + chunk);
+    if (!a.do_sample) {
+        const float pivot = radix_kth_largest_global(S, n, static_cast<uint32_t>(take), hist, sel);
+        uint32_t cg = 0, ce = 0;
+        for (int i = i0; i < i1; ++i) {
+            cg += S[i] > pivot;
+            ce += S[i] == pivot;
+        }
+        uint32_t ng = 0, ne = 0;
+        uint32_t og = block_scan(cg, wtot, &ng);
+        uint32_t oe = block_scan(ce, wtot, &ne);
+        const uint32_t need = static_cast<uint32_t>(take) - ng;  // ties at the pivot, smallest indices first
+        for (int i = i0; i < i1; ++i) {
+            if (S[i] > pivot) ids[og++] = static_cast<uint32_t>(i);
+            else if (S[i] == pivot) {
+                if (oe < need) ids[ng + oe] = static_cast<uint32_t>(i);
+                ++oe;
+            }
+        }
+        __syncthreads();
+        if (t == 0) {
+            // (score desc, index asc): the order std::partial_sort produces with index ties.
+            for (int x = 1; x < take; ++x) {
+                const uint32_t v = ids[x];
+                int y = x - 1;
+                while (y >= 0 && (S[ids[y]] < S[v] || (S[ids[y]] == S[v] && ids[y] > v))) {
+                    ids[y + 1] = ids[y];
+                    --y;
+                }
+                ids[y + 1] = v;
+            }
+            a.status[0] = kOk;
+        }
+    } else {
+        // Finite entries in index order, kept in global scratch (a.list), weights in a.probs.
+        uint32_t c = 0;
+        for (int i = i0; i < i1; ++i) c += finite_f(S[i]);
+        uint32_t F = 0;
+        uint32_t off = block_scan(c, wtot, &F);
+        for (int i = i0; i < i1; ++i)
+            if (finite_f(S[i])) a.list[off++] = static_cast<uint32_t>(i);
+        __syncthreads();
+        if (t == 0) stop_s = 0;
+        uint64_t rng = *a.rng;
+        for (int d = 0; d < take; ++d) {
+            float m = -INFINITY;  // max over the still-available finite entries
+            for (uint32_t j = t; j < F; j += NT) {
+                const uint32_t id = a.list[j];
+                if (!(id & 0x80000000u)) m = fmaxf(m, S[id]);
+            }
+            m = wave_max(m);
+            if (lane == 0) wmax[wave] = m;
+            __syncthreads();
+            if (t == 0) {
+                float g = wmax[0];
+                for (int w = 1; w < NWAVE; ++w) g = fmaxf(g, wmax[w]);
+                mx_s = g;
+            }
+            __syncthreads();
+            const float mx = mx_s;
+            if (mx == -INFINITY) {
+                if (t == 0) a.status[0] = kNoFinite;
+                return;
+            }
+            for (uint32_t j = t; j < F; j += NT) {
+                const uint32_t id = a.list[j];
+                a.probs[j] = (id & 0x80000000u) ? 0.0 : exp(static_cast<double>(S[id] - mx));
+            }
+            __syncthreads();
+            if (t == 0) {
+                double total = 0.0;
+                for (uint32_t j = 0; j < F; ++j) total += a.probs[j];
+                if (total <= 0.0) {
+                    stop_s = kZeroMass;
+                } else {
+                    const double target = splitmix_unit(rng) * total;
+                    double cumulative = 0.0;
+                    uint32_t pick = 0xffffffffu, last = 0xffffffffu;
+                    for (uint32_t j = 0; j < F; ++j) {
+                        const double p = a.probs[j];
+                        if (p <= 0.0) continue;
+                        last = j;
+                        cumulative += p;
+                        if (target < cumulative) {
+                            pick = j;
+                            break;
+                        }
+                    }
+                    if (pick == 0xffffffffu) pick = last;
+                    ids[d] = a.list[pick];
+                    a.list[pick] |= 0x80000000u;
+                }
+            }
+            __syncthreads();
+            if (stop_s) {
+                if (t == 0) a.status[0] = stop_s;
+                return;
+            }
+        }
+        if (t == 0) {
+            *a.rng = rng;
+            // Stable sort by score, descending (std::sort on <= 16 candidates is an insertion sort).
+            for (int x = 1; x < take; ++x) {
+                const uint32_t v = ids[x];
+                int y = x - 1;
+                while (y >= 0 && S[ids[y]] < S[v]) {
+                    ids[y + 1] = ids[y];
+                    --y;
+                }
+                ids[y + 1] = v;
+            }
+            a.status[0] = kOk;
+        }
+    }
+    if (t < take) {
+        const uint32_t id = ids[t];
+        a.cand[t] = BeamCand{id / static_cast<uint32_t>(V), id % static_cast<uint32_t>(V), S[id], 0u};
+    }
+}
+
+}  // namespace
+
+hipError_t launch_beam_scores(const BeamArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(beam_scores_kernel, dim3(a.parents), dim3(NT), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_beam_select(const BeamArgs& a, hipStream_t s) {
+    if (a.take < 1 || a.take > kMaxBeamTake) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(beam_select_kernel, dim3(1), dim3(NT), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace itts

@@ -103,6 +103,30 @@ struct SampleArgs {
 };
 hipError_t launch_sampler(const SampleArgs& a, int batch, hipStream_t s);
 
+// ------------------------------------------------------------------ beam search
+constexpr int kMaxBeamTake = 2 * kMaxBatch;
+struct BeamCand {
+    uint32_t parent, token;
+    float score;
+    uint32_t _pad;
+};
+struct BeamArgs {
+    const float* logits;      // [parents][8194]
+    const uint8_t* seen;      // [parents][8194] repetition sets
+    const float* beam_score;  // [parents]
+    float* all_scores;        // [parents][8194] out of beam_scores, in of beam_select
+    double* probs;            // scratch, >= parents * 8194
+    uint32_t* list;           // scratch, >= parents * 8194
+    uint32_t* status;         // [0] select, [1 + p] scores of parent p
+    uint64_t* rng;            // SplitMix64 state of the search
+    BeamCand* cand;           // [take]
+    int parents, take, do_sample, suppress_stop;
+    float temperature, top_p, penalty;
+    uint32_t top_k, num_beams;
+};
+hipError_t launch_beam_scores(const BeamArgs& a, hipStream_t s);
+hipError_t launch_beam_select(const BeamArgs& a, hipStream_t s);
+
 // ------------------------------------------------------------------ prefill
 struct LnRowsArgs {
     const float* x;
@@ -154,8 +178,10 @@ hipError_t launch_speaker_row(const float* w, const float* b, const float* speak
                               hipStream_t s);
 // Copy row src_rows[b] of x into h[b] (last prefix row of each sequence).
 hipError_t launch_gather_rows(const float* x, const uint32_t* src_rows, float* h, int batch, hipStream_t s);
-// Beam reorder of the row-owner table and seen sets: child c takes parent[c]'s rows 0..n-1 and own row n.
+// Beam reorder: child c (of `children`) takes parent[c]'s row owners for rows 0..n-1 and its
+// repetition set plus token[c]; it owns row n itself.  `parents` rows are staged first, so
+// several children may share a parent.
 hipError_t launch_beam_reorder(uint8_t* table, uint8_t* table_tmp, uint8_t* seen, uint8_t* seen_tmp, const uint32_t* parent,
-                               int beams, uint32_t n, uint32_t cap, hipStream_t s);
+                               const uint32_t* token, int parents, int children, uint32_t n, uint32_t cap, hipStream_t s);
 
 }  // namespace itts

@@ -110,6 +110,12 @@ struct Engine {
     // prefill scratch
     DevBuf<float> px, pxn, pq, patt, pff;
     DevBuf<uint32_t> row_slot, row_pos, last_rows;
+    // beam search scratch
+    DevBuf<float> beam_scores, all_scores;
+    DevBuf<uint32_t> beam_list, d_token;
+    DevBuf<double> beam_probs;
+    DevBuf<BeamCand> cand;
+    DevBuf<uint64_t> beam_rng;
     // API scratch
     DevBuf<float> api_out;
     DevBuf<uint32_t> api_tokens;
@@ -909,8 +915,145 @@ void Engine::generate(const float* prefix, uint32_t rows, const itts_gen_options
     generate_batch({prefix}, {rows}, {c}, max_tokens, codes_out, n_codes, stopped);
 }
 
-void Engine::generate_beams(const float*, uint32_t, const itts_gen_options&, uint32_t, std::vector<uint32_t>&, bool&) {
-    throw std::runtime_error("Beam search is not available in this build");
+// gpt_sampling.cpp:190-245.  Scores, processors and candidate selection run on the device
+// (beam.hip); the child/finish bookkeeping below is the reference's, on the host.  Beam
+// KV is not snapshotted: child c lives in slot c and inherits its parent's rows through
+// the row-owner table (one byte per row), which the attention kernel gathers through.
+void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_options& config, uint32_t maximum,
+                            std::vector<uint32_t>& result, bool& eos) {
+    const uint32_t nbeam = config.num_beams;
+    if (nbeam > max_batch) throw std::invalid_argument("num_beams exceeds the decoder's max_batch");
+    struct Beam {
+        std::vector<uint32_t> codes;
+        float score = 0;
+    };
+    struct Finished {
+        std::vector<uint32_t> codes;
+        double score;
+        bool eos;
+    };
+    std::vector<Finished> finished;
+    const uint32_t take = 2 * nbeam;
+    beam_scores.ensure(kMaxBatch);
+    all_scores.ensure(static_cast<size_t>(kMaxBatch) * kMelVocab);
+    beam_list.ensure(static_cast<size_t>(kMaxBatch) * kMelVocab);
+    beam_probs.ensure(static_cast<size_t>(kMaxBatch) * kMelVocab);
+    cand.ensure(kMaxBeamTake);
+    d_token.ensure(kMaxBatch);
+    beam_rng.ensure(1);
+
+    pinned_state[0] = make_state(config, rows, maximum);
+    upload_states(1);
+    HIP_CHECK(hipEventRecord(ev[0], stream));
+    enqueue_prefill({prefix}, {rows});
+    for (uint32_t b = 1; b < nbeam; ++b)
+        HIP_CHECK(hipMemcpyAsync(logits.p + static_cast<size_t>(b) * kMelVocab, logits.p, kMelVocab * 4, hipMemcpyDeviceToDevice, stream));
+    HIP_CHECK(hipMemsetAsync(table.p, 0, static_cast<size_t>(nbeam) * cap, stream));  // prefix rows live in slot 0
+    HIP_CHECK(hipEventRecord(ev[1], stream));
+    reset_seen(static_cast<int>(nbeam));
+    uint64_t* prng = reinterpret_cast<uint64_t*>(pinned + 62);
+    *prng = config.seed;
+    HIP_CHECK(hipMemcpyAsync(beam_rng.p, prng, 8, hipMemcpyHostToDevice, stream));
+
+    std::vector<Beam> beams(nbeam);
+    for (uint32_t i = 1; i < beams.size(); ++i) beams[i].score = -1e9f;
+    auto finish = [&](const Beam& beam, float score, uint32_t length, bool e) {
+        finished.push_back({beam.codes, score / std::pow(static_cast<double>(std::max(length, 1u)), config.length_penalty), e});
+        std::stable_sort(finished.begin(), finished.end(), [](const auto& x, const auto& y) { return x.score > y.score; });
+        if (finished.size() > nbeam) finished.resize(nbeam);
+    };
+    uint32_t last_rows = rows, steps = 0;
+    std::vector<BeamCand> cands(take);
+    std::vector<uint32_t> st(1 + kMaxBatch);
+    float* pscore = reinterpret_cast<float*>(pinned + 52);
+    uint32_t* ppar = pinned + 32;
+    uint32_t* ptok = pinned + 42;
+    for (uint32_t step_index = 0; step_index < maximum; ++step_index) {
+        const uint32_t P = static_cast<uint32_t>(beams.size());
+        for (uint32_t p = 0; p < P; ++p) pscore[p] = beams[p].score;
+        HIP_CHECK(hipMemcpyAsync(beam_scores.p, pscore, P * 4, hipMemcpyHostToDevice, stream));
+        BeamArgs a{};
+        a.logits = logits.p;
+        a.seen = seen.p;
+        a.beam_score = beam_scores.p;
+        a.all_scores = all_scores.p;
+        a.probs = beam_probs.p;
+        a.list = beam_list.p;
+        a.status = status.p;
+        a.rng = beam_rng.p;
+        a.cand = cand.p;
+        a.parents = static_cast<int>(P);
+        a.take = static_cast<int>(take);
+        a.do_sample = config.do_sample ? 1 : 0;
+        a.suppress_stop = config.suppress_stop ? 1 : 0;
+        a.temperature = config.temperature;
+        a.top_p = config.top_p;
+        a.penalty = config.repetition_penalty;
+        a.top_k = config.top_k;
+        a.num_beams = nbeam;
+        HIP_CHECK(launch_beam_scores(a, stream));
+        HIP_CHECK(launch_beam_select(a, stream));
+        HIP_CHECK(hipMemcpyAsync(cands.data(), cand.p, take * sizeof(BeamCand), hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipMemcpyAsync(st.data(), status.p, (1 + P) * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        for (uint32_t i = 0; i <= P; ++i)
+            if (st[i]) throw std::runtime_error(sampler_message(st[i]));
+        std::vector<Beam> next;
+        uint32_t C = 0;
+        for (uint32_t rank = 0; rank < take; ++rank) {
+            const BeamCand c = cands[rank];
+            const Beam& parent = beams[c.parent];
+            if (c.token == static_cast<uint32_t>(kMelStop)) {
+                if (rank < nbeam) finish(parent, c.score, step_index + 1, true);
+                continue;
+            }
+            if (c.token >= static_cast<uint32_t>(kMelStart)) throw std::runtime_error("Beam generated invalid semantic code");
+            Beam child;
+            child.codes = parent.codes;
+            child.codes.push_back(c.token);
+            child.score = c.score;
+            ppar[C] = c.parent;
+            ptok[C] = c.token;
+            ++C;
+            next.push_back(std::move(child));
+            if (next.size() == nbeam) break;
+        }
+        if (next.empty()) break;
+        if (step_index + 1 < maximum) {
+            const uint32_t n = rows + step_index;  // rows cached before this forward, equal for every beam
+            HIP_CHECK(hipMemcpyAsync(d_parent.p, ppar, C * 4, hipMemcpyHostToDevice, stream));
+            HIP_CHECK(hipMemcpyAsync(d_token.p, ptok, C * 4, hipMemcpyHostToDevice, stream));
+            HIP_CHECK(launch_beam_reorder(table.p, table_tmp.p, seen.p, seen_tmp.p, d_parent.p, d_token.p, static_cast<int>(P),
+                                          static_cast<int>(C), n, cap, stream));
+            for (uint32_t c = 0; c < C; ++c) {
+                SeqState s = make_state(config, rows, maximum);
+                s.n = n;
+                s.position = step_index + 2;
+                s.token = ptok[c];
+                pinned_state[c] = s;
+            }
+            upload_states(static_cast<int>(C));
+            run_step(static_cast<int>(C), gemv_batch_bucket(static_cast<int>(C)), false, true);
+            last_rows = n + 1;
+            ++steps;
+        }
+        beams = std::move(next);
+        if (finished.size() == nbeam &&
+            finished.back().score >= cands[0].score / std::pow(static_cast<double>(step_index + 1), config.length_penalty)) {
+            beams.clear();
+            break;
+        }
+    }
+    HIP_CHECK(hipEventRecord(ev[2], stream));
+    HIP_CHECK(hipStreamSynchronize(stream));
+    HIP_CHECK(hipEventElapsedTime(&timing.prefill_ms, ev[0], ev[1]));
+    HIP_CHECK(hipEventElapsedTime(&timing.decode_ms, ev[1], ev[2]));
+    timing.decode_steps = steps;
+    for (const auto& beam : beams) finish(beam, beam.score, static_cast<uint32_t>(beam.codes.size()), false);
+    if (finished.empty()) throw std::runtime_error("Beam search produced no hypotheses");
+    result = std::move(finished[0].codes);
+    eos = finished[0].eos;
+    cached = last_rows;
 }
 
 }  // namespace itts

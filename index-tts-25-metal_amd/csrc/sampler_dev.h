@@ -1,0 +1,353 @@
+// Device-side pieces of the logits processors and sampler, shared by the decode
+// sampler (sampler.hip) and the beam-search kernels (beam.hip).  One 1024-thread
+// workgroup works on one 8194-entry score row held in LDS.
+//
+// Restated from the reference (src/gpt_sampling.cpp):
+//   run_processors  :28-128  repetition penalty once per distinct history id
+//                            (x<0 ? x*p : x/p), /= T, top-k (k-th largest is the pivot,
+//                            values below it -> -inf, ties survive), top-p (ascending
+//                            (score, index) order, double softmax, drop while the
+//                            cumulative <= 1 - p, keep the top 1, or 2 for beams);
+//   draw_token      :130-165 p_i = exp(double(s_i - max)), total in index order,
+//                            target = u * total, first i with target < cumulative,
+//                            else the last positive one;
+//   splitmix_*      :11-26   SplitMix64.
+// Only ordering-free work runs in parallel (elementwise ops, a radix select for the
+// top-k pivot, index-order compaction, a bitonic sort of survivors).  Every floating-
+// point sum the reference forms sequentially is formed by one thread in the same order.
+#pragma once
+#include "kernels.h"
+
+namespace itts {
+namespace sampling {
+
+constexpr int V = kMelVocab;
+constexpr int NT = 1024;
+constexpr int NWAVE = NT / 64;
+constexpr int IPT = (V + NT - 1) / NT;  // contiguous indices per thread for compaction (9)
+constexpr int kSortMax = 16384;          // next power of two >= V
+constexpr int kSmallProbs = 1024;
+constexpr uint16_t kRemoved = 0x8000;
+
+enum Status : uint32_t {
+    kOk = 0,
+    kTopPEmpty = 1,    // "GPT top_p filtering removed all logits"
+    kZeroMass = 2,     // "GPT sampling probability mass is zero"
+    kNoFinite = 3,     // "GPT sampling received no finite logits"
+    kInvalidCode = 4,  // "GPT generated invalid semantic code"
+};
+
+struct Smem {
+    union {
+        float s[V];
+        uint64_t sortbuf[kSortMax];
+    };
+    uint16_t list[V];  // finite survivors in index order; bit 15 = removed by top-p
+    double probs[kSmallProbs];
+    uint32_t hist[256];
+    uint32_t wtot[NWAVE];
+    float wmax[NWAVE];
+    uint32_t widx[NWAVE];
+    uint32_t sel[2];
+    uint32_t m;
+    uint32_t token;
+    uint32_t status;
+    float mx;
+};
+
+__device__ __forceinline__ uint64_t splitmix_next(uint64_t& state) {
+    uint64_t z = (state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ double splitmix_unit(uint64_t& state) {
+    return static_cast<double>(splitmix_next(state) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+__device__ __forceinline__ bool finite_f(float v) { return fabsf(v) <= 3.402823466e38f; }
+
+// kk-th largest value (1-based) of s[0..V): MSB-first radix select on order-preserving keys.
+__device__ inline float radix_kth_largest(Smem& sm, uint32_t kk) {
+    const int t = threadIdx.x, lane = t & 63;
+    uint32_t prefix = 0, mask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (t < 256) sm.hist[t] = 0;
+        __syncthreads();
+        for (int i = t; i < V; i += NT) {
+            const uint32_t k = float_key(sm.s[i]);
+            if ((k & mask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (t < 64) {
+            uint32_t c[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) c[q] = sm.hist[255 - 4 * lane - q];
+            const uint32_t loc = c[0] + c[1] + c[2] + c[3];
+            uint32_t inc = loc;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += v;
+            }
+            const uint32_t exc = inc - loc;
+            if (exc < kk && kk <= inc) {
+                uint32_t run = exc;
+                int d = -1;
+                uint32_t above = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (d < 0) {
+                        if (run + c[q] >= kk) {
+                            d = 255 - 4 * lane - q;
+                            above = run;
+                        } else {
+                            run += c[q];
+                        }
+                    }
+                }
+                sm.sel[0] = static_cast<uint32_t>(d);
+                sm.sel[1] = above;
+            }
+        }
+        __syncthreads();
+        prefix |= sm.sel[0] << shift;
+        mask |= 0xffu << shift;
+        kk -= sm.sel[1];
+        __syncthreads();
+    }
+    return key_float(prefix);
+}
+
+// Compact finite entries of s into sm.list (index order); returns the count, sets sm.mx.
+__device__ inline uint32_t compact_finite(Smem& sm) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int i0 = t * IPT, i1 = min(V, i0 + IPT);
+    uint32_t c = 0;
+    float mloc = -INFINITY;
+    for (int i = i0; i < i1; ++i) {
+        const float v = sm.s[i];
+        if (finite_f(v)) {
+            ++c;
+            mloc = fmaxf(mloc, v);
+        }
+    }
+    uint32_t inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+    }
+    const float wm = wave_max(mloc);
+    if (lane == 63) sm.wtot[wave] = inc;
+    if (lane == 0) sm.wmax[wave] = wm;
+    __syncthreads();
+    uint32_t off = 0, total = 0;
+    float mx = -INFINITY;
+    for (int w = 0; w < NWAVE; ++w) {
+        if (w < wave) off += sm.wtot[w];
+        total += sm.wtot[w];
+        mx = fmaxf(mx, sm.wmax[w]);
+    }
+    off += inc - c;
+    for (int i = i0; i < i1; ++i)
+        if (finite_f(sm.s[i])) sm.list[off++] = static_cast<uint16_t>(i);
+    if (t == 0) {
+        sm.m = total;
+        sm.mx = mx;
+    }
+    __syncthreads();
+    return total;
+}
+
+// First index of the maximum (std::max_element semantics).
+__device__ inline uint32_t block_argmax(Smem& sm) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    float best = -INFINITY;
+    uint32_t bi = V;
+    for (int i = t; i < V; i += NT) {
+        const float v = sm.s[i];
+        if (v > best || (v == best && static_cast<uint32_t>(i) < bi)) {
+            best = v;
+            bi = static_cast<uint32_t>(i);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        sm.wmax[wave] = best;
+        sm.widx[wave] = bi;
+    }
+    __syncthreads();
+    float b2 = sm.wmax[0];
+    uint32_t i2 = sm.widx[0];
+    for (int w = 1; w < NWAVE; ++w)
+        if (sm.wmax[w] > b2 || (sm.wmax[w] == b2 && sm.widx[w] < i2)) {
+            b2 = sm.wmax[w];
+            i2 = sm.widx[w];
+        }
+    __syncthreads();
+    return i2;
+}
+
+// Ascending bitonic sort of sm.sortbuf[0..n), n a power of two.
+__device__ inline void bitonic_sort(Smem& sm, int n) {
+    const int t = threadIdx.x;
+    if (n <= 64) {
+        if (t < 64) {
+            uint64_t v = t < n ? sm.sortbuf[t] : ~0ull;
+            for (int k = 2; k <= 64; k <<= 1)
+                for (int j = k >> 1; j > 0; j >>= 1) {
+                    const uint64_t o = __shfl_xor(v, j, 64);
+                    const bool lower = (t & j) == 0;
+                    const bool asc = (t & k) == 0;
+                    const uint64_t lo = v < o ? v : o, hi = v < o ? o : v;
+                    v = (lower == asc) ? lo : hi;
+                }
+            if (t < n) sm.sortbuf[t] = v;
+        }
+        __syncthreads();
+        return;
+    }
+    for (int k = 2; k <= n; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int p = t; p < n / 2; p += NT) {
+                const int i = (p / j) * 2 * j + (p % j);
+                const int l = i + j;
+                const bool asc = (i & k) == 0;
+                const uint64_t a = sm.sortbuf[i], c = sm.sortbuf[l];
+                if ((a > c) == asc) {
+                    sm.sortbuf[i] = c;
+                    sm.sortbuf[l] = a;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+
+// gpt_sampling.cpp:28-128 on sm.s (already holding the input scores).  On return:
+//   sm.s holds the processed scores, unless top-p ran with rebuild == false, in which
+//   case sm.s is clobbered and the survivors are described by sm.list (index order,
+//   kRemoved flags), sm.m, sm.mx and P[0..m) (exp(double(s - mx)) of each survivor).
+// *topp_ran tells which.  Returns a Status.
+__device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ seen, float pen, float T, uint32_t top_k,
+                                          float top_p, uint32_t beams, double* P_global, bool rebuild, bool* topp_ran) {
+    const int t = threadIdx.x;
+    *topp_ran = false;
+    if (pen != 1.0f || T != 1.0f) {
+        for (int i = t; i < V; i += NT) {
+            float v = sm.s[i];
+            if (pen != 1.0f && seen[i]) v = v < 0.0f ? v * pen : v / pen;
+            if (T != 1.0f) v = v / T;
+            sm.s[i] = v;
+        }
+        __syncthreads();
+    }
+    if (top_k > 0 && top_k < static_cast<uint32_t>(V)) {
+        const uint32_t k = max(top_k, beams > 1 ? 2u : 1u);
+        const float pivot = radix_kth_largest(sm, k);
+        for (int i = t; i < V; i += NT)
+            if (sm.s[i] < pivot) sm.s[i] = -INFINITY;
+        __syncthreads();
+    }
+    if (!(top_p < 1.0f)) return kOk;
+    *topp_ran = true;
+    const uint32_t m = compact_finite(sm);
+    if (m == 0) return kTopPEmpty;
+    const float mx = sm.mx;
+    double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : P_global;
+    for (uint32_t j = t; j < m; j += NT) P[j] = exp(static_cast<double>(sm.s[sm.list[j]] - mx));
+    // Keys: (score key << 32) | j; j increases with the index, so ties break by index.
+    int n = 64;
+    while (n < static_cast<int>(m)) n <<= 1;
+    uint64_t keys[kSortMax / NT];
+#pragma unroll
+    for (int q = 0; q < kSortMax / NT; ++q) {
+        const int j = t + q * NT;
+        keys[q] = j < static_cast<int>(m) ? (static_cast<uint64_t>(float_key(sm.s[sm.list[j]])) << 32) | static_cast<uint32_t>(j) : ~0ull;
+    }
+    __syncthreads();  // s[] is overwritten by the sort buffer below
+#pragma unroll
+    for (int q = 0; q < kSortMax / NT; ++q) {
+        const int j = t + q * NT;
+        if (j < n) sm.sortbuf[j] = keys[q];
+    }
+    __syncthreads();
+    bitonic_sort(sm, n);
+    if (t == 0) {
+        double total = 0.0;
+        for (uint32_t j = 0; j < m; ++j) total += P[j];
+        if (total <= 0.0) {
+            sm.status = kZeroMass;
+        } else {
+            sm.status = kOk;
+            const double threshold = 1.0 - static_cast<double>(top_p);
+            double cumulative = 0.0;
+            for (uint32_t q = 0; q < m; ++q) {
+                const uint32_t j = static_cast<uint32_t>(sm.sortbuf[q]);
+                cumulative += P[j] / total;
+                if (cumulative <= threshold) sm.list[j] |= kRemoved;
+            }
+            const uint32_t keep = min(m, beams > 1 ? 2u : 1u);
+            for (uint32_t q = m - keep; q < m; ++q) sm.list[static_cast<uint32_t>(sm.sortbuf[q])] &= ~kRemoved;
+        }
+    }
+    __syncthreads();
+    const uint32_t st = sm.status;
+    if (st != kOk || !rebuild) return st;
+    // Rebuild s[] from the sorted keys (the key carries the score).
+#pragma unroll
+    for (int q = 0; q < kSortMax / NT; ++q) {
+        const int j = t + q * NT;
+        keys[q] = j < n ? sm.sortbuf[j] : ~0ull;
+    }
+    __syncthreads();
+    for (int i = t; i < V; i += NT) sm.s[i] = -INFINITY;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kSortMax / NT; ++q) {
+        const uint64_t k = keys[q];
+        if (k == ~0ull) continue;
+        const uint32_t j = static_cast<uint32_t>(k);
+        const uint16_t e = sm.list[j];
+        if (!(e & kRemoved)) sm.s[e & 0x7fff] = key_float(static_cast<uint32_t>(k >> 32));
+    }
+    __syncthreads();
+    return kOk;
+}
+
+// gpt_sampling.cpp:130-165 by thread 0 over the survivors sm.list[0..m) with weights P.
+// Returns the token, or 0xffffffff with *status set when the mass is zero.
+__device__ inline uint32_t draw_token(const Smem& sm, uint32_t m, const double* P, uint64_t& rng, uint32_t* status) {
+    double total = 0.0;
+    for (uint32_t j = 0; j < m; ++j)
+        if (!(sm.list[j] & kRemoved)) total += P[j];
+    if (total <= 0.0) {
+        *status = kZeroMass;
+        return 0xffffffffu;
+    }
+    const double target = splitmix_unit(rng) * total;
+    double cumulative = 0.0;
+    uint32_t last_finite = 0;
+    for (uint32_t j = 0; j < m; ++j) {
+        const uint16_t e = sm.list[j];
+        if (e & kRemoved) continue;
+        const double p = P[j];
+        if (p <= 0.0) continue;
+        last_finite = e;
+        cumulative += p;
+        if (target < cumulative) return e;
+    }
+    return last_finite;
+}
+
+}  // namespace sampling
+}  // namespace itts

@@ -74,27 +74,24 @@ __global__ void gather_rows_kernel(const float* x, const uint32_t* src_rows, flo
         h[static_cast<size_t>(b) * kWidth + c] = x[static_cast<size_t>(src_rows[b]) * kWidth + c];
 }
 
-// Beam reorder: child c inherits parent[c]'s row owners (rows 0..n-1) and repetition set,
-// and owns row n itself.  Two passes through scratch copies so children may share parents.
-__global__ void beam_copy_kernel(const uint8_t* table, uint8_t* table_tmp, const uint8_t* seen, uint8_t* seen_tmp, int beams,
-                                 uint32_t cap) {
+// Beam reorder: child c inherits parent[c]'s row owners (rows 0..n-1) and repetition set
+// (plus its new token) and owns row n itself.  Parents are staged first so children may share them.
+__global__ void beam_stage_kernel(const uint8_t* table, uint8_t* table_tmp, const uint8_t* seen, uint8_t* seen_tmp, uint32_t n,
+                                  uint32_t cap) {
     const int b = blockIdx.y;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < cap; i += gridDim.x * blockDim.x)
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
         table_tmp[static_cast<size_t>(b) * cap + i] = table[static_cast<size_t>(b) * cap + i];
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < static_cast<uint32_t>(kMelVocab); i += gridDim.x * blockDim.x)
         seen_tmp[static_cast<size_t>(b) * kMelVocab + i] = seen[static_cast<size_t>(b) * kMelVocab + i];
 }
 __global__ void beam_apply_kernel(uint8_t* table, const uint8_t* table_tmp, uint8_t* seen, const uint8_t* seen_tmp,
-                                  const uint32_t* parent, uint32_t n, uint32_t cap) {
+                                  const uint32_t* parent, const uint32_t* token, uint32_t n, uint32_t cap) {
     const int c = blockIdx.y;
-    const uint32_t p = parent[c];
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < cap; i += gridDim.x * blockDim.x) {
-        uint8_t v = table_tmp[static_cast<size_t>(p) * cap + i];
-        if (i == n) v = static_cast<uint8_t>(c);
-        if (i <= n) table[static_cast<size_t>(c) * cap + i] = v;
-    }
+    const uint32_t p = parent[c], tok = token[c];
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i <= n; i += gridDim.x * blockDim.x)
+        table[static_cast<size_t>(c) * cap + i] = i == n ? static_cast<uint8_t>(c) : table_tmp[static_cast<size_t>(p) * cap + i];
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < static_cast<uint32_t>(kMelVocab); i += gridDim.x * blockDim.x)
-        seen[static_cast<size_t>(c) * kMelVocab + i] = seen_tmp[static_cast<size_t>(p) * kMelVocab + i];
+        seen[static_cast<size_t>(c) * kMelVocab + i] = i == tok ? 1 : seen_tmp[static_cast<size_t>(p) * kMelVocab + i];
 }
 
 }  // namespace
@@ -137,10 +134,9 @@ hipError_t launch_gather_rows(const float* x, const uint32_t* src_rows, float* h
 }
 
 hipError_t launch_beam_reorder(uint8_t* table, uint8_t* table_tmp, uint8_t* seen, uint8_t* seen_tmp, const uint32_t* parent,
-                               int beams, uint32_t n, uint32_t cap, hipStream_t s) {
-    const dim3 grid(8, beams);
-    hipLaunchKernelGGL(beam_copy_kernel, grid, dim3(256), 0, s, table, table_tmp, seen, seen_tmp, beams, cap);
-    hipLaunchKernelGGL(beam_apply_kernel, grid, dim3(256), 0, s, table, table_tmp, seen, seen_tmp, parent, n, cap);
+                               const uint32_t* token, int parents, int children, uint32_t n, uint32_t cap, hipStream_t s) {
+    hipLaunchKernelGGL(beam_stage_kernel, dim3(8, parents), dim3(256), 0, s, table, table_tmp, seen, seen_tmp, n, cap);
+    hipLaunchKernelGGL(beam_apply_kernel, dim3(8, children), dim3(256), 0, s, table, table_tmp, seen, seen_tmp, parent, token, n, cap);
     return hipGetLastError();
 }
 

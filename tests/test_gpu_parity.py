@@ -236,3 +236,48 @@ def test_full_greedy_128(full, itts, oracle):
     except oracle.OracleError as e:
         exp = str(e)
     assert got == exp
+
+
+# ---------------------------------------------------------------------------- beam search (gpt_sampling.cpp:190-245)
+
+@pytest.fixture(scope="module")
+def beam_small(itts, oracle, small_weights):
+    dec = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=4)
+    orc = oracle.OracleGpt(small_weights, kv_capacity=1024)
+    cond, text = itts.synthetic_prefix_inputs(30, seed=2)
+    return dec, orc, dec.prepare_cond(cond, text, 0)
+
+
+@pytest.mark.parametrize("opts", [
+    dict(do_sample=False, repetition_penalty=1.0, num_beams=3),
+    dict(do_sample=False, repetition_penalty=10.0, num_beams=3),
+    dict(do_sample=True, seed=7, num_beams=3),
+    dict(do_sample=True, seed=9, num_beams=2, top_k=0, top_p=0.9, temperature=1.2),
+    dict(do_sample=False, num_beams=4, length_penalty=1.0, top_k=5),
+])
+def test_beam_search_matches_oracle(beam_small, itts, oracle, opts):
+    dec, orc, prefix = beam_small
+    o = itts.GenerationOptions(**opts)
+    r = dec.generate(prefix, o, 24)
+    codes, stopped = orc.generate(prefix, oracle.options_from(o), 24)
+    assert (r.codes, r.stopped) == (codes, stopped)
+    assert dec.cached_tokens() == orc.cached_tokens()
+
+
+def test_beam_search_needs_capacity(beam_small, itts):
+    dec, _, prefix = beam_small
+    with pytest.raises(itts.InvalidArgument, match="max_batch"):
+        dec.generate(prefix, itts.GenerationOptions(num_beams=5), 4)
+
+
+def test_full_beam3_config3_shape(itts, oracle, full_weights):
+    """Config 3 shape: 32 latents + 80 text ids, 3 beams, repetition penalty 10 (40 codes here)."""
+    dec = itts.GptDecoder(full_weights, kv_capacity=4096, max_batch=3)
+    orc = oracle.OracleGpt(full_weights, kv_capacity=4096)
+    cond, text = itts.synthetic_prefix_inputs(80, seed=3)
+    prefix = orc.prepare_cond(cond, text, 0)
+    assert prefix.size // 1280 == 115
+    o = itts.GenerationOptions(do_sample=False, num_beams=3, length_penalty=0.0, repetition_penalty=10.0, suppress_stop=True)
+    r = dec.generate(prefix, o, 40)
+    codes, stopped = orc.generate(prefix, oracle.options_from(o), 40)
+    assert (r.codes, r.stopped) == (codes, stopped)

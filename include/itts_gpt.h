@@ -132,12 +132,16 @@ int itts_gpt_sample(itts_gpt* h, const float* processed, uint32_t vocab, uint64_
                     uint32_t* tokens);
 
 /* Timing of the last prefill / generate call on the handle's stream, from HIP
- * events (milliseconds). */
+ * events (milliseconds).  decode_path: which kernels ran the last decode step or
+ * generate loop, ITTS_PATH_MULTI (one launch per GEMV / attention pass, replayed
+ * from a captured graph) or ITTS_PATH_STEP (one persistent launch per token). */
+#define ITTS_PATH_MULTI 0u
+#define ITTS_PATH_STEP 1u
 typedef struct {
     float prefill_ms;
     float decode_ms;
     uint32_t decode_steps;
-    uint32_t _pad;
+    uint32_t decode_path;
 } itts_gpt_timing;
 int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
 
@@ -146,7 +150,8 @@ int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
  * returns the mean launch duration from HIP events and the algorithmic bytes moved per
  * launch.  which: 0 c_attn GEMV (+LayerNorm, K/V append), 1 attn.c_proj GEMV (+residual),
  * 2 mlp.c_fc GEMV (+LayerNorm, GELU), 3 mlp.c_proj GEMV (+residual), 4 mel_head GEMV
- * (+ln_f, final_norm), 5 decode attention at 753 cached rows. */
+ * (+ln_f, final_norm), 5 decode attention at 753 cached rows, 6 the persistent
+ * whole-step kernel at 752 cached rows (batch 1, FP32 weights only). */
 int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t iters, float* avg_ms, double* bytes_per_launch);
 
 /* Deterministic N(mean, std^2) fill for synthetic weights and inputs: value i is

@@ -36,7 +36,7 @@ DEVICE_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
-SOURCES = ["decode.hip", "sampler.hip", "beam.hip", "prefill.hip", "util.hip", "runtime.hip"]
+SOURCES = ["decode.hip", "step.hip", "sampler.hip", "beam.hip", "prefill.hip", "util.hip", "runtime.hip"]
 
 
 def _run(cmd: list[str]) -> None:

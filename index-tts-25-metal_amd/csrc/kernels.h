@@ -80,6 +80,36 @@ constexpr int kAttnMaxSplits = 64;   // splits per (sequence, head) at most
 // Split pass (grid splits x 20 x batch) then merge pass (grid 20 x batch).
 hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 
+// ------------------------------------------------------------------ persistent decode step
+// One launch per token for a single sequence (step.hip): grid = one 512-thread
+// workgroup per CU, all resident together; workgroups hand vectors over through the exchange buffer
+// (tagged 64-bit slots, kStepExchange of them, zero-initialised once).
+constexpr int kStepThreads = 512;
+constexpr int kStepExchange = kWidth + kQkv + kWidth + kWidth + kFfn + kHeads * kAttnMaxSplits * 68;
+struct StepArgs {
+    const void* w;            // weight slab, fp32 or bf16
+    size_t layer_stride;      // elements per layer block (c_attn, c_proj, c_fc, mlp.c_proj)
+    size_t off_head;          // element offset of mel_head
+    const float* params;      // [layers][kParLayer]
+    const float* head;        // [kHeadPar]
+    const float* mel_emb;
+    const float* mel_pos;
+    float* kv;                // cache of sequence slot 0
+    size_t kv_layer_stride;   // floats per layer
+    size_t kv_v_off;
+    uint32_t kv_cap;
+    int layers;
+    int splits;               // attention splits at most (as the multi-kernel path)
+    const SeqState* state;    // sequence 0
+    uint64_t* xch;            // exchange slots
+    float* logits;            // [8194]
+    uint32_t epoch;           // tag base of this launch (fresh per launch, never 0)
+    uint32_t* err;            // set to 1 when a hand-off wait gives up
+};
+bool step_fits(int grid);
+hipError_t step_occupancy(bool bf16, int* blocks_per_cu);
+hipError_t launch_step(const StepArgs& a, int grid, bool bf16, hipStream_t s);
+
 // ------------------------------------------------------------------ sampler
 enum SampleMode : int {
     kModeDecode = 0,      // processors from state options + seen mask, choose, advance state

@@ -123,6 +123,14 @@ struct Engine {
     SeqState* pinned_state = nullptr;
     int splits = 16;
     bool use_graphs = true;  // ITTS_GPT_GRAPHS=0: launch the same kernels eagerly (profilers)
+    // Persistent single-sequence step (step.hip): one launch per token.  Opt-in with
+    // ITTS_GPT_PERSISTENT=1; otherwise batch 1 uses the multi-kernel graph path.
+    bool step_ok = false;
+    int step_grid = 0;
+    size_t per_layer = 0;       // weight elements per layer block
+    DevBuf<uint64_t> xch;       // tagged exchange slots
+    DevBuf<uint32_t> step_err;  // hand-off timeout flag
+    uint32_t epoch = 8;         // tag base of the next launch
     std::map<std::tuple<int, int, bool, bool>, hipGraphExec_t> graphs;
     hipEvent_t ev[4] = {};
     uint32_t cached = 0;
@@ -203,8 +211,7 @@ struct Engine {
         if (!layers) throw std::runtime_error("Missing tensor: gpt.gpt.h.0.attn.c_attn.weight");
 
         // Weight slab.
-        const size_t per_layer = static_cast<size_t>(kQkv) * kWidth + static_cast<size_t>(kWidth) * kWidth +
-                                 2 * static_cast<size_t>(kFfn) * kWidth;
+        per_layer = static_cast<size_t>(kQkv) * kWidth + static_cast<size_t>(kWidth) * kWidth + 2 * static_cast<size_t>(kFfn) * kWidth;
         const size_t total = per_layer * layers + static_cast<size_t>(kMelVocab) * kWidth;
         slab.alloc(total * elt);
         DevBuf<float> staging;
@@ -296,8 +303,72 @@ struct Engine {
         seen_tmp.alloc((B + 1) * kMelVocab);
         table.alloc(B * cap);
         table_tmp.alloc(B * cap);
+        init_step();
         HIP_CHECK(hipStreamSynchronize(stream));
     }
+
+    // The persistent step runs when one 512-thread workgroup fits per CU (the grid is one
+    // workgroup per CU, all resident together), the per-CU weight slices fit the kernel's
+    // register tiles (step_fits), weights are FP32 and attention tiles stay <= 64 rows
+    // (cap <= 4096).
+    void init_step() {
+        const char* pe = std::getenv("ITTS_GPT_PERSISTENT");
+        if (!pe || std::strcmp(pe, "1") != 0 || bf16 || cap > 4096) return;
+        int dev = 0, cus = 0, occ = 0;
+        HIP_CHECK(hipGetDevice(&dev));
+        HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        HIP_CHECK(step_occupancy(false, &occ));
+        if (occ < 1 || !step_fits(cus)) return;
+        xch.alloc(kStepExchange);
+        HIP_CHECK(hipMemsetAsync(xch.p, 0, xch.n * sizeof(uint64_t), stream));
+        step_err.alloc(1);
+        HIP_CHECK(hipMemsetAsync(step_err.p, 0, sizeof(uint32_t), stream));
+        step_grid = cus;
+        step_ok = true;
+    }
+
+    StepArgs step_args() {
+        // Each launch takes a fresh range of 8*(layers+1) tags; before the 32-bit counter
+        // wraps, the exchange is cleared and numbering restarts.
+        const uint32_t span = 8u * static_cast<uint32_t>(layers + 1);
+        if (epoch > 0xF0000000u - span) {
+            HIP_CHECK(hipMemsetAsync(xch.p, 0, xch.n * sizeof(uint64_t), stream));
+            epoch = 8;
+        }
+        StepArgs s{};
+        s.w = slab.p;
+        s.layer_stride = per_layer;
+        s.off_head = off_head;
+        s.params = params.p;
+        s.head = head_params.p;
+        s.mel_emb = mel_emb.p;
+        s.mel_pos = mel_pos.p;
+        s.kv = kv.p;
+        s.kv_layer_stride = kv_layer_stride;
+        s.kv_v_off = kv_v_off;
+        s.kv_cap = cap;
+        s.layers = layers;
+        s.splits = splits;
+        s.state = state.p;
+        s.xch = xch.p;
+        s.logits = logits.p;
+        s.epoch = epoch;
+        s.err = step_err.p;
+        epoch += span;
+        return s;
+    }
+
+    // Raises (and clears) a hand-off timeout reported by the persistent step; call after a sync.
+    void check_step_error() {
+        if (!step_ok) return;
+        uint32_t e = 0;
+        HIP_CHECK(hipMemcpy(&e, step_err.p, sizeof(e), hipMemcpyDeviceToHost));
+        if (e) {
+            HIP_CHECK(hipMemset(step_err.p, 0, sizeof(uint32_t)));
+            throw std::runtime_error("GPT decode step: a workgroup hand-off timed out");
+        }
+    }
+    bool persistent(int nseq, bool use_table) const { return step_ok && nseq == 1 && !use_table; }
 
     // ---------------------------------------------------------------- forward pieces
     GemvArgs gemv_base(int nseq) const {
@@ -414,6 +485,13 @@ struct Engine {
 
     // Runs one step (forward [+ sampler]) as a replay of its captured graph, or eagerly.
     void run_step(int nseq, int nb, bool sampler, bool use_table) {
+        if (persistent(nseq, use_table)) {
+            timing.decode_path = ITTS_PATH_STEP;
+            HIP_CHECK(launch_step(step_args(), step_grid, bf16, stream));
+            if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
+            return;
+        }
+        timing.decode_path = ITTS_PATH_MULTI;
         if (use_graphs) {
             HIP_CHECK(hipGraphLaunch(graph(nseq, nb, sampler, use_table), stream));
             return;
@@ -595,6 +673,7 @@ struct Engine {
         run_step(1, 1, false, false);
         HIP_CHECK(hipMemcpyAsync(out_logits, logits.p, kMelVocab * 4, hipMemcpyDeviceToHost, stream));
         HIP_CHECK(hipStreamSynchronize(stream));
+        check_step_error();
         cached++;
     }
 
@@ -628,7 +707,7 @@ struct Engine {
     // are in logits[0..nseq): sampler, then (forward + sampler) graph replays.
     void decode_loop(int nseq, uint32_t max_tokens) {
         const int nb = gemv_batch_bucket(nseq);
-        if (use_graphs) (void)graph(nseq, nb, true, false);  // captured before any work is queued
+        if (use_graphs && !persistent(nseq, false)) (void)graph(nseq, nb, true, false);  // captured before any work is queued
         HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
         constexpr uint32_t kChunk = 16;
         uint32_t launched = 0;
@@ -676,6 +755,7 @@ struct Engine {
         HIP_CHECK(hipStreamSynchronize(stream));
         HIP_CHECK(hipEventElapsedTime(&timing.prefill_ms, ev[0], ev[1]));
         HIP_CHECK(hipEventElapsedTime(&timing.decode_ms, ev[1], ev[2]));
+        check_step_error();
         uint32_t steps = 0;
         for (int b = 0; b < nseq; ++b) {
             const SeqState& s = pinned_state[b];
@@ -822,8 +902,9 @@ struct Engine {
     // Launches one decode kernel kind `iters` times (layer l = i % layers, so consecutive
     // launches stream different weights) between two HIP events on the handle's stream.
     void bench_kernel(int which, int batch, int iters, float* avg_ms, double* bytes) {
-        if (!layers || which < 0 || which > 5 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
+        if (!layers || which < 0 || which > 6 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
             throw std::invalid_argument("Invalid kernel benchmark request");
+        if (which == 6 && (!step_ok || batch != 1)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
         const int nb = gemv_batch_bucket(batch);
         std::vector<SeqState> st(batch);
         for (int b = 0; b < batch; ++b) {
@@ -864,6 +945,9 @@ struct Engine {
                 case 4:
                     enqueue_head(batch, nb);
                     break;
+                case 6:
+                    HIP_CHECK(launch_step(step_args(), step_grid, bf16, stream));
+                    break;
                 default: {
                     AttnArgs t{};
                     t.q = q.p; t.kv = kv.p; t.kv_slot_stride = kv_slot_stride; t.kv_layer_off = kv_layer_off(l); t.kv_v_off = kv_v_off;
@@ -883,7 +967,12 @@ struct Engine {
         const double e = static_cast<double>(elt);
         const double rows[5] = {kQkv, kWidth, kFfn, kWidth, kMelVocab};
         const double cols[5] = {kWidth, kWidth, kWidth, kFfn, kWidth};
-        if (which < 5) {
+        if (which == 6) {
+            // the whole forward: every weight byte once + K/V rows read and the new row written
+            const double weights = static_cast<double>(slab.n) + 4.0 * (params.n + head_params.n) + 2.0 * kWidth * 4;
+            *bytes = weights + static_cast<double>(layers) * 2.0 * (st[0].n + 1) * kWidth * 4.0;
+            check_step_error();
+        } else if (which < 5) {
             // weights + bias + input rows (+ LayerNorm params) + outputs, per launch
             *bytes = rows[which] * cols[which] * e + rows[which] * 4.0 + batch * cols[which] * 4.0 + batch * rows[which] * 4.0 +
                      ((which == 0 || which == 2) ? 2.0 * kWidth * 4 : 0.0) + (which == 4 ? 4.0 * kWidth * 4 : 0.0) +

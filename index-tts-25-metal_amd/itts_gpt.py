@@ -67,7 +67,7 @@ class _Options(C.Structure):
 
 
 class _Timing(C.Structure):
-    _fields_ = [("prefill_ms", C.c_float), ("decode_ms", C.c_float), ("decode_steps", C.c_uint32), ("_pad", C.c_uint32)]
+    _fields_ = [("prefill_ms", C.c_float), ("decode_ms", C.c_float), ("decode_steps", C.c_uint32), ("decode_path", C.c_uint32)]
 
 
 def _load() -> C.CDLL:
@@ -282,9 +282,10 @@ class GptDecoder:
     def last_timing(self) -> dict:
         t = _Timing()
         self._check(_lib.itts_gpt_last_timing(self._h, C.byref(t)))
-        return {"prefill_ms": t.prefill_ms, "decode_ms": t.decode_ms, "decode_steps": t.decode_steps}
+        return {"prefill_ms": t.prefill_ms, "decode_ms": t.decode_ms, "decode_steps": t.decode_steps,
+                "decode_path": "step" if t.decode_path == 1 else "multi"}
 
-    KERNELS = ("gemv_c_attn", "gemv_attn_proj", "gemv_c_fc", "gemv_mlp_proj", "gemv_mel_head", "attention")
+    KERNELS = ("gemv_c_attn", "gemv_attn_proj", "gemv_c_fc", "gemv_mlp_proj", "gemv_mel_head", "attention", "step")
 
     def bench_kernel(self, which: str, iters: int = 240, batch: int = 1) -> dict:
         """Mean duration (HIP events) and algorithmic bytes of one decode kernel kind."""

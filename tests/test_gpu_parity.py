@@ -281,3 +281,55 @@ def test_full_beam3_config3_shape(itts, oracle, full_weights):
     r = dec.generate(prefix, o, 40)
     codes, stopped = orc.generate(prefix, oracle.options_from(o), 40)
     assert (r.codes, r.stopped) == (codes, stopped)
+
+
+# ---------------------------------------------------------------------------- persistent step kernel (step.hip)
+
+@pytest.fixture(scope="module")
+def both_paths(itts, small_weights):
+    """The same 2-layer model on the persistent step kernel and on the multi-kernel path."""
+    import os
+
+    old = os.environ.get("ITTS_GPT_PERSISTENT")
+    try:
+        os.environ["ITTS_GPT_PERSISTENT"] = "0"
+        multi = itts.GptDecoder(small_weights, kv_capacity=1024)
+        os.environ["ITTS_GPT_PERSISTENT"] = "1"
+        step = itts.GptDecoder(small_weights, kv_capacity=1024)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT"] = old
+    return step, multi
+
+
+@pytest.mark.parametrize("n_text", [10, 40, 300, -900])
+def test_persistent_step_bitwise_equals_multikernel(both_paths, itts, n_text):
+    """Same FMA orders, LayerNorm reduction, attention tiles and merge: logits equal bit for bit
+    (KV lengths spanning 1 to 15 attention splits; -900 = a raw 900-row random prefix)."""
+    step, multi = both_paths
+    if n_text > 0:
+        cond, text = itts.synthetic_prefix_inputs(n_text, seed=n_text)
+        prefix = step.prepare_cond(cond, text, 0)
+    else:
+        prefix = itts.synthetic_normal(-n_text * 1280, 77, 0.0, 0.5)
+    assert np.array_equal(step.prefill(prefix), multi.prefill(prefix))
+    for i, code in enumerate([5, 8191, 0, 4096, 17, 300]):
+        a = step.step(code, i + 2)
+        assert step.last_timing()["decode_path"] == "step"
+        b = multi.step(code, i + 2)
+        assert multi.last_timing()["decode_path"] == "multi"
+        assert np.array_equal(a, b), f"step {i}: max diff {np.max(np.abs(a - b))}"
+
+
+def test_persistent_generate_equals_multikernel(both_paths, itts):
+    step, multi = both_paths
+    cond, text = itts.synthetic_prefix_inputs(60, seed=5)
+    prefix = step.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(do_sample=True, seed=11, suppress_stop=True)
+    a = step.generate(prefix, o, 96)
+    assert step.last_timing()["decode_path"] == "step"
+    b = multi.generate(prefix, o, 96)
+    assert (a.codes, a.stopped) == (b.codes, b.stopped)
+    assert step.cached_tokens() == multi.cached_tokens()

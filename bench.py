@@ -1,16 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the GPT semantic-token loop on one MI355X.
 
-Workload (one "step"): the full-length sampled decode of the 24-layer d=1280 FP32 GPT at
-batch 1 -- prefix of 32 conditioning latents ~N(0,1)*0.5 plus 120 text ids (155 prefix
-rows), prefill, then 600 codes sampled with temperature 0.8, top_k 30, top_p 0.8,
-repetition penalty 10, SplitMix64 seed 42; the KV cache grows to 754 rows.  Random-init
-weights N(0, 0.02).  Codes 8192/8193 are suppressed so every step yields exactly 600
-codes (suppress_stop; applied identically by the CPU oracle).
+Headline workload (one "step" of the contract = one whole generate() call): full-length
+sampled decode of the 24-layer d=1280 FP32 GPT at batch 1 -- prefix of 32 conditioning
+latents ~N(0,1)*0.5 plus 120 text ids (155 prefix rows), prefill, then 600 codes sampled
+with temperature 0.8, top_k 30, top_p 0.8, repetition penalty 10, SplitMix64 seed 42; the
+KV cache grows to 754 rows.  Random-init weights N(0, 0.02).  Codes 8192/8193 are
+suppressed so every call yields exactly 600 codes (suppress_stop; the CPU oracle applies
+the same rule).
 
-Prints one JSON line: tokens/s of whole generate() calls (prefill included) with inputs
-resident on the device, the roofline of the dominant kernel (mlp.c_proj GEMV, 26 MB of
-weights per launch) from HIP-event timing, and the CPU oracle timed on a bounded sample.
+Prints ONE JSON line: tokens/s of whole generate() calls (prefill included) with inputs
+resident on the device; the roofline of the dominant decode kernel from HIP events; the
+CPU oracle timed on a bounded sample; and, under "extras", the other workloads of the
+same model: beam search with 3 beams, long-context greedy decode to a 2047-row cache
+(attention GB/s reported separately), and 8 ragged sampled sequences with FP32 and BF16
+weights.
+
+    python bench.py                      # everything (a few minutes)
+    python bench.py --no-extras --no-cpu # headline only
+    python bench.py --kernel-only gemv_c_fc --iters 240   # one kernel kind, for profilers
 """
 import argparse
 import json
@@ -27,6 +35,7 @@ sys.path.insert(0, str(ROOT / "index-tts-25-metal_amd"))
 HBM_PEAK_GBS = 8000.0
 WEIGHT_BYTES_PER_TOKEN = 1_931_051_016  # FP32 weights + biases + LayerNorm + mel_head + 2 embedding rows
 KV_BYTES_PER_ROW = 245_760              # 24 layers x (K + V) x 1280 x 4 B
+METRIC = "GPT decode tokens/s @bs1 FP32 + % of HBM roofline; beam-3 tokens/s"
 
 
 def decode_bytes(prefix_rows: int, tokens: int) -> float:
@@ -38,17 +47,16 @@ def decode_bytes(prefix_rows: int, tokens: int) -> float:
     return total
 
 
-def cpu_baseline(weights, prefix, opts, sample_steps: int):
+def cpu_baseline(weights, prefix, sample_steps: int):
+    """The FP32 CPU oracle (OpenMP over output rows) on a bounded sample of the same decode."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     orc = oracle.OracleGpt(weights, kv_capacity=4096)
-    o = oracle.options_from(opts)
     t0 = time.perf_counter()
     orc.prefill(prefix)
     t1 = time.perf_counter()
-    lg = None
     code = 100
     for i in range(sample_steps):
         lg = orc.step(code, i + 2)
@@ -60,8 +68,76 @@ def cpu_baseline(weights, prefix, opts, sample_steps: int):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle prefill of the 155-row prefix ({t1 - t0:.2f} s) + {sample_steps} decode steps of the same 24-layer FP32 model",
+        "sample": f"oracle prefill of the 155-row prefix ({t1 - t0:.2f} s) then {sample_steps} decode steps "
+                  f"(KV 155..{155 + sample_steps}) of the same 24-layer FP32 model, {t2 - t1:.1f} s",
     }
+
+
+def timed(fn, reps: int):
+    out, times = None, []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+    return out, times
+
+
+def extras(it, dec, weights):
+    """Beam-3, long-context and batch-8 (FP32, BF16) workloads of the same model."""
+    res = {}
+    # Beam search, 3 beams: 32 latents + 80 text ids, 400 codes, length penalty 0, repetition penalty 10.
+    cond, text = it.synthetic_prefix_inputs(80, seed=3)
+    prefix = dec.prepare_cond(cond, text, 0)
+    o = it.GenerationOptions(num_beams=3, length_penalty=0.0, repetition_penalty=10.0, seed=7, suppress_stop=True)
+    dec.generate(prefix, o, 32)
+    r, times = timed(lambda: dec.generate(prefix, o, 400), 2)
+    tm = dec.last_timing()
+    steps = tm["decode_steps"]
+    res["beam3"] = {
+        "codes": len(r.codes), "seconds": round(min(times), 4),
+        "beam_steps_per_s": round(steps / (tm["decode_ms"] * 1e-3), 2),
+        "beam_tokens_per_s": round(3 * steps / (tm["decode_ms"] * 1e-3), 2),
+        "prefix_rows": prefix.size // 1280,
+    }
+    # Long context: 32 latents + 200 text ids, greedy to the 1815 mel positions (KV -> 2047).
+    cond, text = it.synthetic_prefix_inputs(200, seed=4)
+    prefix = dec.prepare_cond(cond, text, 0)
+    o = it.GenerationOptions(do_sample=False, repetition_penalty=1.0, suppress_stop=True)
+    r, times = timed(lambda: dec.generate(prefix, o, 1813), 2)
+    tm = dec.last_timing()
+    rows = prefix.size // 1280
+    att = dec.bench_kernel("attention", iters=240, cached_rows=2046)
+    res["long_context"] = {
+        "codes": len(r.codes), "kv_rows": rows + len(r.codes) - 1,
+        "decode_tokens_per_s": round((len(r.codes) - 1) / (tm["decode_ms"] * 1e-3), 2),
+        "step_algorithmic_GBps": round(decode_bytes(rows, len(r.codes)) / (tm["decode_ms"] * 1e-3) / 1e9, 1),
+        "attention_at_2047_rows": {"avg_us": round(att["avg_ms"] * 1e3, 2),
+                                   "GBps": round(att["bytes"] / (att["avg_ms"] * 1e-3) / 1e9, 1)},
+    }
+    # 8 independent sequences: text lengths U[24, 200] (seed 7), 300 sampled codes each.
+    rng = np.random.default_rng(7)
+    prefixes, opts = [], []
+    for b in range(8):
+        cond, text = it.synthetic_prefix_inputs(int(rng.integers(24, 201)), seed=100 + b)
+        prefixes.append(dec.prepare_cond(cond, text, 0))
+        opts.append(it.GenerationOptions(seed=1000 + b, suppress_stop=True))
+    for dtype in ("f32", "bf16"):
+        d = dec if dtype == "f32" else it.GptDecoder(weights, kv_capacity=4096, max_batch=8, weight_dtype="bf16")
+        d.generate_batch(prefixes, opts, 16)
+        r, times = timed(lambda: d.generate_batch(prefixes, opts, 300), 2)
+        tm = d.last_timing()
+        total = sum(len(x.codes) for x in r)
+        res[f"batch8_{dtype}"] = {
+            "codes": total, "seconds": round(min(times), 4),
+            "tokens_per_s": round(total / min(times), 2),
+            "decode_tokens_per_s": round(8 * (tm["decode_steps"] - 1) / (tm["decode_ms"] * 1e-3), 2),
+        }
+        if dtype == "bf16":
+            ref = dec.prefill(prefixes[0])
+            got = d.prefill(prefixes[0])
+            res["batch8_bf16"]["prefill_logit_maxabs_vs_f32"] = float(np.max(np.abs(got - ref)))
+            d.close()
+    return res
 
 
 def main() -> int:
@@ -70,8 +146,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=600)
-    ap.add_argument("--cpu-steps", type=int, default=24)
+    ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs)")
+    ap.add_argument("--iters", type=int, default=240)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
@@ -80,8 +159,15 @@ def main() -> int:
     import itts_gpt as it
 
     weights = it.make_synthetic_weights(layers=24, seed=0)
+    dec = it.GptDecoder(weights, kv_capacity=4096, max_batch=8)
+    if args.kernel_only:
+        k = dec.bench_kernel(args.kernel_only, iters=args.iters)
+        print(json.dumps({"kernel": args.kernel_only, "iters": args.iters, "avg_us": round(k["avg_ms"] * 1e3, 3),
+                          "bytes_per_launch": k["bytes"], "GBps": round(k["bytes"] / (k["avg_ms"] * 1e-3) / 1e9, 1)}),
+              flush=True)
+        return 0
+
     cond, text = it.synthetic_prefix_inputs(120, seed=42)
-    dec = it.GptDecoder(weights, kv_capacity=4096)
     prefix = dec.prepare_cond(cond, text, 0)
     rows = prefix.size // 1280
     opts = it.GenerationOptions(do_sample=True, seed=42, temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=10.0,
@@ -101,25 +187,29 @@ def main() -> int:
         if codes is not None:
             assert r.codes == codes, "generate() is not deterministic"
         codes = r.codes
+    path = dec.last_timing()["decode_path"]
     total = sum(times)
     value = args.tokens * args.steps / total
     dmean = float(np.mean(decode_ms))
-    step_bytes = decode_bytes(rows, args.tokens)
-    step_gbs = step_bytes / (dmean * 1e-3) / 1e9
+    step_gbs = decode_bytes(rows, args.tokens) / (dmean * 1e-3) / 1e9
 
-    kern = dec.bench_kernel("gemv_mlp_proj", iters=240)
+    # Dominant decode kernel: the whole-step kernel on the persistent path, else the
+    # mlp.c_fc GEMV (the largest share of the multi-kernel step's time).
+    dominant = "step" if path == "step" else "gemv_c_fc"
+    kern = dec.bench_kernel(dominant, iters=args.iters if dominant != "step" else 60)
     achieved = kern["bytes"] / (kern["avg_ms"] * 1e-3) / 1e9
-    kernels = {k: dec.bench_kernel(k, iters=240 if k != "gemv_mel_head" else 48) for k in it.GptDecoder.KERNELS}
-    extra = {k: {"avg_us": round(v["avg_ms"] * 1e3, 2), "GB/s": round(v["bytes"] / (v["avg_ms"] * 1e-3) / 1e9, 1)}
-             for k, v in kernels.items()}
+    names = [k for k in it.GptDecoder.KERNELS if k not in ("copy",) and (k != "step" or path == "step")]
+    kernels = {k: dec.bench_kernel(k, iters=240 if k not in ("gemv_mel_head", "step") else 48) for k in names}
+    per_kernel = {k: {"avg_us": round(v["avg_ms"] * 1e3, 2), "GBps": round(v["bytes"] / (v["avg_ms"] * 1e-3) / 1e9, 1)}
+                  for k, v in kernels.items()}
 
     traffic = None
-    pmc = ROOT / "profiles" / "gemv_mlp_proj_traffic.json"
+    pmc = ROOT / "profiles" / f"{dominant}_traffic.json"
     if pmc.exists():
-        traffic = json.loads(pmc.read_text()).get("bytes_per_launch")
+        traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
 
     line = {
-        "metric": "GPT decode tokens/s @bs1 FP32 + % of HBM roofline; beam-3 tokens/s",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -134,16 +224,18 @@ def main() -> int:
         "config": {
             "workload": "IndexTTS-2.5 GPT 24L d1280 FP32, batch 1, prefix 32 latents + 120 text ids (155 rows), "
                         "600 sampled codes (T0.8 k30 p0.8 rep10 seed42), KV to 754",
-            "batch": 1, "prefix_rows": rows, "tokens": args.tokens,
+            "batch": 1, "prefix_rows": rows, "tokens": args.tokens, "decode_path": path,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_mlp_proj (mlp.c_proj 1280x5120 GEMV + residual)",
+            "kernel": dominant,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "bytes_per_launch": kern["bytes"],
+            "avg_us": round(kern["avg_ms"] * 1e3, 3),
         },
         "decode": {
             "prefill_ms": round(float(np.mean(prefill_ms)), 3),
@@ -152,11 +244,13 @@ def main() -> int:
             "step_algorithmic_GBps": round(step_gbs, 1),
             "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         },
-        "kernels": extra,
+        "kernels": per_kernel,
     }
+    if not args.no_extras:
+        line["extras"] = extras(it, dec, weights)
     del dec
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(weights, prefix, opts, args.cpu_steps)
+        line["cpu_baseline"] = cpu_baseline(weights, prefix, args.cpu_steps)
     print(json.dumps(line), flush=True)
     return 0
 

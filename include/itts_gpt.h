@@ -150,9 +150,11 @@ int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
  * returns the mean launch duration from HIP events and the algorithmic bytes moved per
  * launch.  which: 0 c_attn GEMV (+LayerNorm, K/V append), 1 attn.c_proj GEMV (+residual),
  * 2 mlp.c_fc GEMV (+LayerNorm, GELU), 3 mlp.c_proj GEMV (+residual), 4 mel_head GEMV
- * (+ln_f, final_norm), 5 decode attention at 753 cached rows, 6 the persistent
- * whole-step kernel at 752 cached rows (batch 1, FP32 weights only). */
-int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t iters, float* avg_ms, double* bytes_per_launch);
+ * (+ln_f, final_norm), 5 decode attention, 6 the persistent whole-step kernel (batch 1,
+ * FP32 weights only), 7 a 256 MiB device-to-device copy (reference for traffic counters).
+ * Attention and the step kernel run with `cached_rows` rows in the cache (0 -> 752). */
+int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t cached_rows, uint32_t iters, float* avg_ms,
+                          double* bytes_per_launch);
 
 /* Deterministic N(mean, std^2) fill for synthetic weights and inputs: value i is
  * a Box-Muller transform of two SplitMix64 outputs keyed by (seed, i), so the

@@ -83,6 +83,9 @@ int main(int argc, char** argv) {
         return 1;
     } catch (const std::invalid_argument&) {
     }
+    opt.num_beams = 3;  // beam search through the reference-form decoder (10 beam slots)
+    auto rb = gpt.generate(prefix, opt, 6);
+    std::printf("{\"beam_codes\":%zu,\"beam_stopped\":%d}\n", rb.codes.size(), rb.stopped ? 1 : 0);
     auto scores = itts25::apply_gpt_sampling_processors(std::vector<float>(8194, 0.5f), {1, 8192}, itts25::GenerationOptions{});
     std::printf("{\"processed\":%zu}\n", scores.size());
     return 0;

@@ -47,8 +47,11 @@ public:
         const std::vector<float>* data;
     };
 
+    // The reference accepts num_beams up to 10 on any decoder (gpt_sampling.cpp:172-173),
+    // so the reference-form constructor provisions 10 KV slots (10 x 503 MB at capacity 4096).
     template <class Weights, class Context>
-    GptDecoder(Weights& weights, Context& /*device context, unused*/) : GptDecoder(collect(weights)) {}
+    GptDecoder(Weights& weights, Context& /*device context, unused*/) : GptDecoder(collect(weights), &kReferenceConfig) {}
+    static constexpr itts_gpt_config kReferenceConfig{4096, ITTS_MAX_BATCH, ITTS_WEIGHTS_F32, 0};
     explicit GptDecoder(const std::vector<Tensor>& tensors, const itts_gpt_config* config = nullptr);
     ~GptDecoder();
     GptDecoder(const GptDecoder&) = delete;

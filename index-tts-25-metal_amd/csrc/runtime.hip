@@ -901,16 +901,22 @@ struct Engine {
     // ---------------------------------------------------------------- measurement
     // Launches one decode kernel kind `iters` times (layer l = i % layers, so consecutive
     // launches stream different weights) between two HIP events on the handle's stream.
-    void bench_kernel(int which, int batch, int iters, float* avg_ms, double* bytes) {
-        if (!layers || which < 0 || which > 6 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
+    void bench_kernel(int which, int batch, uint32_t cached_rows, int iters, float* avg_ms, double* bytes) {
+        if (!layers || which < 0 || which > 7 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
             throw std::invalid_argument("Invalid kernel benchmark request");
         if (which == 6 && (!step_ok || batch != 1)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
+        if (!cached_rows) cached_rows = 752;
+        if (cached_rows + 1 >= cap) throw std::invalid_argument("Invalid kernel benchmark request");
+        if (which == 7) {
+            bench_copy(iters, avg_ms, bytes);
+            return;
+        }
         const int nb = gemv_batch_bucket(batch);
         std::vector<SeqState> st(batch);
         for (int b = 0; b < batch; ++b) {
             itts_gen_options o;
             itts_gen_options_default(&o);
-            st[b] = make_state(o, std::min<uint32_t>(cap - 2, 752), 2);
+            st[b] = make_state(o, cached_rows, 2);
             st[b].token = 1;
             st[b].position = 2;
         }
@@ -980,6 +986,23 @@ struct Engine {
         } else {
             *bytes = static_cast<double>(batch) * 2.0 * (st[0].n + 1) * kWidth * 4.0;  // K and V rows read
         }
+    }
+
+    // Device-to-device copy of 256 MiB of the weight slab (a plain copy kernel of known
+    // size, the reference point for HBM traffic counters): bytes = read + written.
+    void bench_copy(int iters, float* avg_ms, double* bytes) {
+        const size_t n = std::min<size_t>(slab.n, size_t(256) << 20);
+        DevBuf<uint8_t> dst;
+        dst.alloc(n);
+        HIP_CHECK(hipMemcpyAsync(dst.p, slab.p, n, hipMemcpyDeviceToDevice, stream));
+        HIP_CHECK(hipEventRecord(ev[0], stream));
+        for (int i = 0; i < iters; ++i) HIP_CHECK(hipMemcpyAsync(dst.p, slab.p, n, hipMemcpyDeviceToDevice, stream));
+        HIP_CHECK(hipEventRecord(ev[1], stream));
+        HIP_CHECK(hipEventSynchronize(ev[1]));
+        float ms = 0;
+        HIP_CHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        *avg_ms = ms / iters;
+        *bytes = 2.0 * static_cast<double>(n);
     }
 
     // ---------------------------------------------------------------- beams
@@ -1279,8 +1302,11 @@ int itts_gpt_sample(itts_gpt* h, const float* processed, uint32_t vocab, uint64_
     return guarded(h, [&] { h->e.sample(processed, vocab, rng_state, draws, tokens); });
 }
 
-int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t iters, float* avg_ms, double* bytes_per_launch) {
-    return guarded(h, [&] { h->e.bench_kernel(which, static_cast<int>(batch), static_cast<int>(iters), avg_ms, bytes_per_launch); });
+int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t cached_rows, uint32_t iters, float* avg_ms,
+                          double* bytes_per_launch) {
+    return guarded(h, [&] {
+        h->e.bench_kernel(which, static_cast<int>(batch), cached_rows, static_cast<int>(iters), avg_ms, bytes_per_launch);
+    });
 }
 
 int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out) {

@@ -95,7 +95,7 @@ def _load() -> C.CDLL:
         "itts_gpt_apply_processors": (C.c_int, [P, f32p, u32, u32p, u32, C.POINTER(_Options), f32p]),
         "itts_gpt_sample": (C.c_int, [P, f32p, u32, C.POINTER(C.c_uint64), u32, u32p]),
         "itts_gpt_last_timing": (C.c_int, [P, C.POINTER(_Timing)]),
-        "itts_gpt_bench_kernel": (C.c_int, [P, i32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
+        "itts_gpt_bench_kernel": (C.c_int, [P, i32, u32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
         "itts_synthetic_normal": (None, [f32p, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
     }
     for name, (res, args) in sig.items():
@@ -285,13 +285,15 @@ class GptDecoder:
         return {"prefill_ms": t.prefill_ms, "decode_ms": t.decode_ms, "decode_steps": t.decode_steps,
                 "decode_path": "step" if t.decode_path == 1 else "multi"}
 
-    KERNELS = ("gemv_c_attn", "gemv_attn_proj", "gemv_c_fc", "gemv_mlp_proj", "gemv_mel_head", "attention", "step")
+    KERNELS = ("gemv_c_attn", "gemv_attn_proj", "gemv_c_fc", "gemv_mlp_proj", "gemv_mel_head", "attention", "step", "copy")
 
-    def bench_kernel(self, which: str, iters: int = 240, batch: int = 1) -> dict:
-        """Mean duration (HIP events) and algorithmic bytes of one decode kernel kind."""
+    def bench_kernel(self, which: str, iters: int = 240, batch: int = 1, cached_rows: int = 0) -> dict:
+        """Mean duration (HIP events, back-to-back launches) and algorithmic bytes of one decode
+        kernel kind; attention and "step" run with `cached_rows` cached rows (0 -> 752)."""
         ms = C.c_float()
         by = C.c_double()
-        self._check(_lib.itts_gpt_bench_kernel(self._h, self.KERNELS.index(which), int(batch), int(iters), C.byref(ms), C.byref(by)))
+        self._check(_lib.itts_gpt_bench_kernel(self._h, self.KERNELS.index(which), int(batch), int(cached_rows), int(iters),
+                                               C.byref(ms), C.byref(by)))
         return {"avg_ms": float(ms.value), "bytes": float(by.value)}
 
     # Processors / sampler on this handle's stream.

@@ -24,4 +24,5 @@ def test_shim_runs_on_gpu():
     lines = [json.loads(l) for l in out.stdout.splitlines() if l.startswith("{")]
     assert lines[0]["rows"] == 3 + 6 + 1  # 3 conditioning rows + [0, 5, 17, 300, 42, 1] + mel start
     assert lines[0]["codes"] + lines[0]["stopped"] >= 1
-    assert lines[1]["processed"] == 8194
+    assert lines[1]["beam_codes"] + lines[1]["beam_stopped"] >= 1
+    assert lines[2]["processed"] == 8194

@@ -87,15 +87,75 @@ struct WLoad<uint16_t> {
     }
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Wave reductions: the xor butterfly over distances 32, 16, 8, 4, 2, 1 (each lane combines
+// its value with lane ^ d's), so every lane ends with the same result.  The exchanges run
+// on the VALU instead of the LDS crossbar (ds_bpermute): distance 32 and 16 with gfx950's
+// v_permlane32_swap / v_permlane16_swap, 8 with DPP row_ror:8, 4 with two bank-masked DPP
+// row shifts, 2 and 1 with DPP quad permutes.
+//
+// permlane*_swap(a, b) returns {a with its upper half (32) / odd rows (16) replaced by b's
+// lower half / even rows, b with its lower half / even rows replaced by a's upper half /
+// odd rows}; the element-wise sum of the two is the distance-32 (16) pair sum of a in the
+// lower half (even rows) and of b in the upper half (odd rows).  Passing a == b gives one
+// butterfly step; passing two different values reduces two rows at once.
+__device__ __forceinline__ float xsum32(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xsum16(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xmax32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xmax16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+// value of lane ^ 8, ^ 4, ^ 2, ^ 1
+__device__ __forceinline__ float lane_x8(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)); }
+__device__ __forceinline__ float lane_x4(float v) {
+    int t = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x104, 0xF, 0x5, false);  // banks 0, 2: lane + 4
+    t = __builtin_amdgcn_update_dpp(t, __float_as_int(v), 0x114, 0xF, 0xA, false);                    // banks 1, 3: lane - 4
+    return __int_as_float(t);
+}
+__device__ __forceinline__ float lane_x2(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)); }
+__device__ __forceinline__ float lane_x1(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)); }
+// distances 8, 4, 2, 1 (within 16-lane rows)
+__device__ __forceinline__ float row16_sum(float v) {
+    v += lane_x8(v);
+    v += lane_x4(v);
+    v += lane_x2(v);
+    v += lane_x1(v);
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+// distances 1, 2, 4, 8: the sum over each aligned group of 16 lanes (attention's q.k)
+__device__ __forceinline__ float sum16_up(float v) {
+    v += lane_x1(v);
+    v += lane_x2(v);
+    v += lane_x4(v);
+    v += lane_x8(v);
     return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    const float u = xsum32(v, v);
+    return row16_sum(xsum16(u, u));
+}
+// Two rows at once, each with wave_sum's pairings: lanes 0-31 end with sum(a), 32-63 with sum(b).
+__device__ __forceinline__ float wave_sum2(float a, float b) {
+    const float v = xsum32(a, b);
+    return row16_sum(xsum16(v, v));
+}
+// Four rows at once: lanes 0-15 end with sum(a), 16-31 sum(c), 32-47 sum(b), 48-63 sum(d).
+__device__ __forceinline__ float wave_sum4(float a, float b, float c, float d) { return row16_sum(xsum16(xsum32(a, b), xsum32(c, d))); }
+__device__ __forceinline__ float wave_max(float v) {
+    v = xmax16(xmax32(v));
+    v = fmaxf(v, lane_x8(v));
+    v = fmaxf(v, lane_x4(v));
+    v = fmaxf(v, lane_x2(v));
+    return fmaxf(v, lane_x1(v));
 }
 
 // Order-preserving map float -> uint32 (larger float -> larger key).

@@ -224,10 +224,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         d = __builtin_fmaf(q4.y, k4[i].y, d);
         d = __builtin_fmaf(q4.z, k4[i].z, d);
         d = __builtin_fmaf(q4.w, k4[i].w, d);
-        d += __shfl_xor(d, 1, 64);
-        d += __shfl_xor(d, 2, 64);
-        d += __shfl_xor(d, 4, 64);
-        d += __shfl_xor(d, 8, 64);
+        d = sum16_up(d);
         const bool valid = p0 + g + 16 * i < p1;
         sc[i] = valid ? d * 0.125f : -INFINITY;
         mloc = fmaxf(mloc, sc[i]);

@@ -2,31 +2,42 @@
 // final_norm and the mel_head GEMV) as ONE launch of one 512-thread workgroup per CU,
 // instead of 6 launches per layer.
 //
-// Residency: the kernel needs > 128 VGPRs per thread, so a CU holds one of its
-// workgroups at most, and the grid is the CU count: on a GPU with free CUs every
-// workgroup is resident at once.  A plain launch is used rather than a cooperative one:
-// ROCm grants cooperative launches to one process per GPU at a time, which would make
-// a second process on the GPU fail.  Workgroups that start late (CUs held by other
-// work) only delay the hand-offs; every wait is bounded and reports an error instead
-// of hanging.
-//
 // Why: at batch 1 each GEMV launch carries 2.5-3 us of fixed cost (dispatch, first HBM
-// round trip, end-of-kernel cache flush) and the step has ~146 of them, so the launch
-// chain, not HBM, bounds the token rate.  Here a phase boundary is a data hand-off
-// between workgroups instead of a kernel boundary:
-//   * every value that crosses workgroups (h, q|k|v, attention partials, attention
-//     output, hmid, ffn activations) is written as ONE 64-bit agent-scope atomic store
-//     {float bits, epoch} and read with agent-scope atomic loads that are retried until
-//     the epoch matches.  The tag makes each element self-validating: no counters, no
-//     fences, no cache writeback/invalidate (a fence-based grid barrier costs ~14 us on
-//     gfx950, a tagged hand-off ~2 us);
-//   * each phase first issues the loads of its weight slice (registers), then waits for
-//     its input vector, so the HBM stream overlaps the hand-off latency;
-//   * a workgroup never waits for its own stores, so nothing drains the weight loads.
-// Epochs: base + 8*layer + kind, with a fresh base per launch (host-side counter), so
-// stale values from earlier launches or layers never match.  Each exchange vector has a
-// single buffer: a producer of layer l+1's value can only run after every workgroup has
-// consumed layer l's value (every phase consumes every producer of the phase before).
+// round trip, end-of-kernel cache flush) and the multi-kernel step has 146 of them, so
+// the launch chain, not HBM, bounds the token rate.
+//
+// Structure of a workgroup (one per CU):
+//   * waves 4..7 are LOADERS: they walk this workgroup's whole weight stream for the step
+//     (per layer: its rows of c_attn, the K/V rows of its attention tiles, its rows of
+//     attn.c_proj, mlp.c_fc, mlp.c_proj; then its mel_head rows) in 5 KB chunks, load each
+//     chunk into registers (8 chunks per loader wave in flight or waiting) and copy it into
+//     a 24-chunk LDS ring as soon as its slot is free.  Loaders never wait on other
+//     workgroups, and the register stage lets HBM keep streaming the next phase's rows
+//     while the ring is full and the compute waves wait for a hand-off;
+//   * waves 0..3 COMPUTE: they wait for each phase's input vector from the other
+//     workgroups, form LayerNorms, take their rows' weights from the ring, and publish
+//     outputs.  Row k of a phase slice belongs to compute wave k % 4; attention tiles use
+//     all four waves;
+//   * ring hand-shake, all in LDS: loader w publishes done[w] = (last chunk it landed)+1
+//     (chunks w, w+4, w+8, ... are its own), compute wave c publishes need[c] = the first
+//     chunk it may still read; a loader writes chunk x only when x < min(need) + 24.
+//     A compute wave never waits for a chunk 24 or more past its own need, so a loader
+//     blocked on ring space always has a compute wave able to move need forward.
+// Hand-offs between workgroups: every value that crosses workgroups (h, q|k|v, attention
+// partials, attention output, hmid, FFN activations) is ONE 64-bit agent-scope store
+// {float bits, epoch}, read with agent-scope loads that are retried until the epoch
+// matches.  The tag makes each element self-validating: no counters, fences or cache
+// maintenance (a fence-based grid barrier measured ~14 us on gfx950, a tagged hand-off
+// ~2 us).  Epochs: base + 8*layer + kind with a fresh base per launch, so stale values
+// of earlier launches or layers never match.  One buffer per exchange vector suffices:
+// a producer of layer l+1's value only runs after every workgroup consumed layer l's.
+//
+// Residency: 155 KB of LDS per workgroup allows one workgroup per CU and the grid is the
+// CU count, so on a GPU with free CUs every workgroup is resident at once.  A plain
+// launch is used rather than a cooperative one: ROCm grants cooperative launches to one
+// process per GPU at a time, which would make a second process on the GPU fail.
+// Workgroups that start late only delay the hand-offs; every wait is bounded and reports
+// an error instead of hanging.
 //
 // Arithmetic is that of the multi-kernel path (decode.hip) operation for operation: the
 // same per-row FMA order (lane l takes 16-byte chunks l, l+64, ... then a xor-butterfly),
@@ -43,12 +54,17 @@ namespace itts {
 namespace {
 
 constexpr int kST = kStepThreads;  // 512
-constexpr int kSW = kST / 64;       // waves per workgroup
-constexpr int kSH = kST / 256;      // 256-thread attention groups per workgroup
-constexpr unsigned kSpinLimit = 1u << 20;
-// Rows per wave held in registers, per phase, for one workgroup per CU on 256 CUs
-// (step_fits checks the grid against these).
-constexpr int kRQkv = 2, kRProj = 1, kRFc = 3, kRFc2 = 1, kRHead = 5;
+constexpr int kCT = 256;           // compute threads: waves 0..3
+constexpr int kCW = kCT / 64;      // compute waves
+constexpr int kLW = (kST - kCT) / 64;  // loader waves
+constexpr int kLines = 5;          // 1 KB lines per chunk
+constexpr int kChunkF = kLines * 256;  // floats per chunk (one 1280-wide row)
+constexpr int kRing = 24;          // chunks in the LDS ring
+constexpr int kSlots = 8;          // chunks staged in registers per loader wave
+constexpr int kKvRowsPerChunk = kChunkF / kHeadDim;  // 20 cached rows of one head
+constexpr unsigned kSpinLimit = 1u << 20;     // global polls (~1 us each)
+constexpr unsigned kLdsSpinLimit = 1u << 24;  // LDS polls (~0.1 us each)
+static_assert(kCW == 4 && kLW == 4, "role split");
 
 // Exchange layout (uint64 slots).
 constexpr int kXh = 0;
@@ -58,70 +74,114 @@ constexpr int kXhmid = kXattn + kWidth;
 constexpr int kXff = kXhmid + kWidth;
 constexpr int kXpart = kXff + kFfn;
 static_assert(kXpart + kHeads * kAttnMaxSplits * 68 == kStepExchange, "exchange layout");
-static_assert(kFfn % kST == 0 && kST >= 256 && kST % 256 == 0, "thread layout");
 
 enum Kind : uint32_t { kEpXh = 0, kEpQkv = 1, kEpPart = 2, kEpAttn = 3, kEpHmid = 4, kEpFf = 5 };
 
 __device__ __forceinline__ uint64_t xld(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-// base + 32-bit unsigned element offset (lets the compiler use a scalar base + one VGPR)
+// base + 32-bit unsigned element offset (a scalar base plus one VGPR per address)
 __device__ __forceinline__ uint64_t xld(const uint64_t* base, int off) { return xld(base + static_cast<uint32_t>(off)); }
 __device__ __forceinline__ void xst(uint64_t* p, uint32_t epoch, float v) {
     __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Reads N tagged values (all loads issued first), retrying each until its epoch is `e`.
-// A bounded wait: past kSpinLimit retries the error flag is raised and the thread stops
-// waiting for the rest of the launch (the host reports the failure).
+// N tagged values: issue() sends all loads, wait() retries the stale ones until their epoch
+// is `e` (one retry loop for all N).  Splitting the two lets a wave do LDS work while the
+// loads are in flight.  A bounded wait: past kSpinLimit retries the error flag is raised
+// and the thread stops waiting for the rest of the launch.
+template <int N>
+struct XRead {
+    uint64_t v[N];
+    __device__ __forceinline__ void issue(const uint64_t* base, const int (&idx)[N], const bool (&use)[N], uint32_t e) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = use[i] ? xld(base, idx[i]) : (static_cast<uint64_t>(e) << 32);
+    }
+    __device__ __forceinline__ void wait(const uint64_t* base, const int (&idx)[N], uint32_t e, float (&out)[N], uint32_t* err,
+                                         bool& failed) {
+        unsigned spins = 0;
+#pragma clang loop unroll(disable)
+        while (true) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < N; ++i) ok &= static_cast<uint32_t>(v[i] >> 32) == e;
+            if (ok) break;
+            if (failed || ++spins > kSpinLimit) {
+                if (!failed) atomicOr(err, 1u);
+                failed = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (static_cast<uint32_t>(v[i] >> 32) != e) v[i] = xld(base, idx[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = __uint_as_float(static_cast<uint32_t>(v[i]));
+    }
+};
 template <int N>
 __device__ __forceinline__ void xread(const uint64_t* base, const int (&idx)[N], const bool (&use)[N], uint32_t e, float (&out)[N],
                                       uint32_t* err, bool& failed) {
-    uint64_t v[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = use[i] ? xld(base, idx[i]) : (static_cast<uint64_t>(e) << 32);
-    // One retry loop for all N (per-element loops would each keep the caller's state live).
+    XRead<N> r;
+    r.issue(base, idx, use, e);
+    r.wait(base, idx, e, out, err, failed);
+}
+
+// threadIdx.x through an empty asm: per-thread offsets derived from it are recomputed in
+// each phase instead of being hoisted out of the layer loop and held live across phases.
+__device__ __forceinline__ int opaque_tid() {
+    int t = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// LDS hand-shake words.  A publish only has to follow this wave's earlier LDS accesses,
+// so it waits lgkmcnt(0) and stores relaxed: a release store would also wait vmcnt(0),
+// i.e. for every load in flight (a loader's whole pipeline of staged loads, or a compute
+// wave's pending global stores).
+constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt/expcnt untouched
+__device__ __forceinline__ uint32_t lds_ld(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void lds_st(uint32_t* p, uint32_t v) {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Ring hand-shake words and the compute-wave barrier counter (an LDS object apart from
+// the ring).
+struct Ctl {
+    uint32_t done[kLW];  // loader w: 1 + last chunk index landed (its chunks are w, w+4, ...)
+    uint32_t need[kCW];  // compute wave c: first chunk it may still read
+    uint32_t bar;        // compute-wave barrier arrivals
+};
+
+// Barrier of the 4 compute waves (the loader waves never join it).
+__device__ __forceinline__ void cbar(Ctl& ctl, uint32_t& gen, uint32_t* err, bool& failed) {
+    gen += kCW;
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this wave's LDS writes are done
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&ctl.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     unsigned spins = 0;
-#pragma clang loop unroll(disable)
-    while (true) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < N; ++i) ok &= static_cast<uint32_t>(v[i] >> 32) == e;
-        if (ok) break;
-        if (failed || ++spins > kSpinLimit) {
+    while (lds_ld(&ctl.bar) < gen) {
+        if (failed || ++spins > kLdsSpinLimit) {
             if (!failed) atomicOr(err, 1u);
             failed = true;
             break;
         }
         __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int i = 0; i < N; ++i)
-            if (static_cast<uint32_t>(v[i] >> 32) != e) v[i] = xld(base, idx[i]);
     }
-#pragma unroll
-    for (int i = 0; i < N; ++i) out[i] = __uint_as_float(static_cast<uint32_t>(v[i]));
 }
 
-// threadIdx.x through an empty asm: per-thread offsets derived from it are recomputed in
-// each phase instead of being hoisted out of the layer loop and held live across all phases.
-__device__ __forceinline__ int opaque_tid() {
-    int t = static_cast<int>(threadIdx.x);
-    asm volatile("" : "+v"(t)::"memory");
-    return t;
-}
-
-// LayerNorm of one 1280-wide row held by threads 0..255 (value tid + 256 i), in the order
-// of ln_block<1, 5> (common.h): wave butterfly, then the 4 wave partials in order.  Every
-// thread of the workgroup calls it (it contains workgroup barriers).
-__device__ __forceinline__ void ln256(float (&v)[5], const float* __restrict__ g, const float* __restrict__ be, float* red, int tid) {
+// LayerNorm of one 1280-wide row held by the 256 compute threads (value tid + 256 i), in
+// the order of ln_block<1, 5> (common.h): wave butterfly, then the 4 wave partials in order.
+__device__ __forceinline__ void ln256(float (&v)[5], const float (&g)[5], const float (&be)[5], float* red, int tid, Ctl& ctl,
+                                      uint32_t& gen, uint32_t* err, bool& failed) {
     const int lane = tid & 63, wave = tid >> 6;
-    const bool act = tid < 256;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 5; ++i) s += v[i];
     s = wave_sum(s);
-    if (act && lane == 0) red[wave] = s;
-    __syncthreads();
+    if (lane == 0) red[wave] = s;
+    cbar(ctl, gen, err, failed);
     const float mean = (((red[0] + red[1]) + red[2]) + red[3]) / float(kWidth);
-    __syncthreads();
+    cbar(ctl, gen, err, failed);
     s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
@@ -129,61 +189,44 @@ __device__ __forceinline__ void ln256(float (&v)[5], const float* __restrict__ g
         s += d * d;
     }
     s = wave_sum(s);
-    if (act && lane == 0) red[wave] = s;
-    __syncthreads();
+    if (lane == 0) red[wave] = s;
+    cbar(ctl, gen, err, failed);
     const float var = (((red[0] + red[1]) + red[2]) + red[3]) / float(kWidth);
     const float inv = 1.0f / sqrtf(var + kLnEps);
-    if (act) {
+#pragma unroll
+    for (int i = 0; i < 5; ++i) v[i] = (v[i] - mean) * inv * g[i] + be[i];
+    cbar(ctl, gen, err, failed);
+}
+// gamma/beta of this thread's 5 LayerNorm columns (tid + 256 i), loaded ahead of the input.
+struct LnPar {
+    float g[5], b[5];
+    __device__ __forceinline__ void load(const float* __restrict__ gp, const float* __restrict__ bp, int tid) {
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
-            const int c = tid + 256 * i;
-            v[i] = (v[i] - mean) * inv * g[c] + be[c];
+            g[i] = gp[tid + 256 * i];
+            b[i] = bp[tid + 256 * i];
         }
     }
-    __syncthreads();
-}
+};
+// Lane holding row k0 + 4 t's sum after wave_sum4 (rows k0 + 4 t, t = 0..3): lanes 0, 32,
+// 16, 48 for t = 0, 1, 2, 3; for wave_sum2 (rows k0, k0 + 4): lanes 0 and 32.
+__device__ __forceinline__ int row_of_lane4(int lane) { return (lane >> 5) + 2 * ((lane >> 4) & 1); }
 
-// Weight rows of this workgroup's slice, wave w holding local rows w, w+8, ... (MAXR of
-// them), each as J 16-byte chunks per lane (chunk j*64 + lane of the row).
-template <typename WT, int J, int MAXR>
-struct Rows {
-    using LD = WLoad<WT>;
-    typename LD::vec w[MAXR][J];
-    int r0, cnt;  // first global row of the slice, rows in the slice (may be <= 0)
-
-    __device__ __forceinline__ void load(const WT* __restrict__ W, int rows, int wave, int lane) {
-        const int per = (rows + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
-        r0 = static_cast<int>(blockIdx.x) * per;
-        cnt = min(per, rows - r0);
+// Bias of the row this lane will hold in each of a wave's first NG row groups of a phase
+// slice (group g = rows wave + G g + 4 t, G = 16 for 1280-wide rows in groups of four, 8 for
+// 5120-wide rows in pairs), loaded while the wave waits for the phase's input so that no row
+// waits on a dependent HBM load.  Later groups load their bias when used.
+template <int NG, bool kWide>
+struct LaneBias {
+    float v[NG];
+    __device__ __forceinline__ void load(const float* __restrict__ b, int cnt, int wave, int lane) {
+        const bool holder = kWide ? (lane & 31) == 0 : (lane & 15) == 0;
+        const int t = kWide ? lane >> 5 : row_of_lane4(lane);
 #pragma unroll
-        for (int r = 0; r < MAXR; ++r) {
-            const int lr = wave + kSW * r;
-            if (lr < cnt) {
-                const uint32_t row = static_cast<uint32_t>(r0 + lr);
-#pragma unroll
-                for (int j = 0; j < J; ++j) w[r][j] = LD::load(W, row * (J * 64) + static_cast<uint32_t>(j * 64 + lane));
-            }
+        for (int g = 0; g < NG; ++g) {
+            const int k = wave + (kWide ? 8 : 16) * g + 4 * t;
+            v[g] = holder && k < cnt ? b[k] : 0.0f;
         }
-    }
-    // acc[r] = sum over the row of w * xs, in the multi-kernel GEMV's order.
-    __device__ __forceinline__ void dot(const float* xs, float (&acc)[MAXR], int wave, int lane) const {
-#pragma unroll
-        for (int r = 0; r < MAXR; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const float4 x4 = *reinterpret_cast<const float4*>(xs + (j * 64 + lane) * 4);
-#pragma unroll
-            for (int r = 0; r < MAXR; ++r) {
-                if (wave + kSW * r >= cnt) continue;
-                const float4 w4 = LD::to_f4(w[r][j]);
-                acc[r] = __builtin_fmaf(w4.x, x4.x, acc[r]);
-                acc[r] = __builtin_fmaf(w4.y, x4.y, acc[r]);
-                acc[r] = __builtin_fmaf(w4.z, x4.z, acc[r]);
-                acc[r] = __builtin_fmaf(w4.w, x4.w, acc[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < MAXR; ++r) acc[r] = wave_sum(acc[r]);
     }
 };
 
@@ -191,82 +234,408 @@ __device__ __forceinline__ int live_splits_dev(int L, int max_splits) {
     return min(max_splits, max(1, (L + kAttnSplitRows - 1) / kAttnSplitRows));
 }
 
+// This workgroup's share of the step, identical in every wave.
+struct Plan {
+    int G, b;
+    uint32_t n;  // cached rows before this step (the new row goes to row n)
+    int L, S, ntiles, chunk_rows, rounds;
+    int q0, qn, p0, pn, f0, fn, g0, gn, h0, hn;  // row slices: c_attn, c_proj, c_fc, mlp.c_proj, mel_head
+    int att_chunks, layer_chunks;
+    int o_att, o_proj, o_fc, o_fc2;  // chunk offsets inside a layer
+
+    __device__ static void slice(int rows, int G, int b, int& r0, int& cnt) {
+        const int per = (rows + G - 1) / G;
+        r0 = b * per;
+        cnt = max(0, min(per, rows - r0));
+    }
+    // Attention tile of round rd: head h, split s, first row t0, cached rows R (< n) in it.
+    __device__ __forceinline__ bool tile(int rd, int& h, int& s, int& t0, int& R) const {
+        const int t = b + G * rd;
+        if (t >= ntiles) return false;
+        h = t % kHeads;
+        s = t / kHeads;
+        t0 = s * chunk_rows;
+        const int t1 = min(L, t0 + chunk_rows);
+        R = max(0, min(t1, static_cast<int>(n)) - t0);
+        return true;
+    }
+    __device__ __forceinline__ static int kv_chunks(int R) { return (R + kKvRowsPerChunk - 1) / kKvRowsPerChunk; }
+
+    __device__ __forceinline__ void init(uint32_t n_, int splits) {
+        G = static_cast<int>(gridDim.x);
+        b = static_cast<int>(blockIdx.x);
+        n = n_;
+        L = static_cast<int>(n) + 1;
+        S = live_splits_dev(L, splits);
+        ntiles = kHeads * S;
+        chunk_rows = (L + S - 1) / S;
+        rounds = (ntiles + G - 1) / G;
+        slice(kQkv, G, b, q0, qn);
+        slice(kWidth, G, b, p0, pn);
+        slice(kFfn, G, b, f0, fn);
+        slice(kWidth, G, b, g0, gn);
+        slice(kMelVocab, G, b, h0, hn);
+        att_chunks = 0;
+        for (int rd = 0; rd < rounds; ++rd) {
+            int h, s, t0, R;
+            if (tile(rd, h, s, t0, R)) att_chunks += 2 * kv_chunks(R);
+        }
+        o_att = qn;
+        o_proj = o_att + att_chunks;
+        o_fc = o_proj + pn;
+        o_fc2 = o_fc + fn;
+        layer_chunks = o_fc2 + 4 * gn;
+    }
+};
+
 struct Smem {
-    float xs[kFfn];      // phase input (normalised where a LayerNorm precedes the GEMV)
+    union {
+        float xs[kFfn];                             // phase input (normalised where a LayerNorm precedes the GEMV)
+        float mpart[kAttnMaxSplits][2 + kHeadDim];  // gathered attention partials of one head (merge)
+    };
     float hraw[kWidth];  // layer input h (residual of attn.c_proj)
     float mraw[kWidth];  // hmid (residual of mlp.c_proj)
     float red[4];
-    float redm[kSH][4], reds[kSH][4];
-    float accs[kSH][16][kHeadDim + 4];
+    float redm[4], reds[4];
+    float accs[16][kHeadDim + 4];
     float mwm[4], mwden[4];
     float mwnum[4][kHeadDim];
-    float mpart[kAttnMaxSplits][2 + kHeadDim];  // gathered attention partials of one head
 };
 
-template <typename WT>
+// ------------------------------------------------------------------ loader waves
+
+// Lane's source addresses of the 5 lines of chunk r of layer l of this workgroup's stream
+// (l == layers: chunk r of its mel_head rows).  Line k of a chunk lands at ring line k,
+// lane i's 16 bytes at +16 i.
+__device__ __forceinline__ void chunk_src(const StepArgs& a, const Plan& P, const float* W, int l, int r, int lane,
+                                          const float* (&src)[kLines]) {
+    const float* base;
+    if (l >= a.layers) {
+        base = W + a.off_head + static_cast<size_t>(P.h0 + r) * kWidth;
+    } else {
+        const float* wl = W + static_cast<size_t>(l) * a.layer_stride;
+        if (r < P.o_att) {
+            base = wl + static_cast<size_t>(P.q0 + r) * kWidth;
+        } else if (r < P.o_proj) {
+            // attention tile chunks: K chunks 0..kc-1 then V chunks, 20 cached rows each,
+            // lane l covers row 4 k + l / 16 of line k, 16 bytes (l % 16) of it
+            int q = r - P.o_att, h = 0, s = 0, t0 = 0, R = 0, kc = 0;
+            for (int rd = 0; rd < P.rounds; ++rd) {
+                if (!P.tile(rd, h, s, t0, R)) continue;
+                kc = Plan::kv_chunks(R);
+                if (q < 2 * kc) break;
+                q -= 2 * kc;
+            }
+            const bool is_v = q >= kc;
+            const int j = is_v ? q - kc : q;
+            const float* kvb = a.kv + static_cast<size_t>(l) * a.kv_layer_stride + (is_v ? a.kv_v_off : 0) +
+                               static_cast<size_t>(h) * a.kv_cap * kHeadDim;
+#pragma unroll
+            for (int k = 0; k < kLines; ++k) {
+                int row = kKvRowsPerChunk * j + 4 * k + (lane >> 4);  // tile-local row
+                if (row >= R) row = 0;                                 // clamped: loaded, never read
+                src[k] = kvb + static_cast<size_t>(t0 + row) * kHeadDim + (lane & 15) * 4;
+            }
+            return;
+        } else if (r < P.o_fc) {
+            base = wl + static_cast<size_t>(kQkv) * kWidth + static_cast<size_t>(P.p0 + r - P.o_proj) * kWidth;
+        } else if (r < P.o_fc2) {
+            base = wl + static_cast<size_t>(kQkv + kWidth) * kWidth + static_cast<size_t>(P.f0 + r - P.o_fc) * kWidth;
+        } else {
+            const int q = r - P.o_fc2;  // mlp.c_proj rows are 5120 wide: 4 chunks each
+            base = wl + static_cast<size_t>(kQkv + kWidth + kFfn) * kWidth + static_cast<size_t>(P.g0 + (q >> 2)) * kFfn +
+                   (q & 3) * kChunkF;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kLines; ++k) src[k] = base + k * 256 + lane * 4;
+}
+
+// Loader wave lw streams chunks lw, lw + 4, lw + 8, ... of the workgroup's sequence.  Each
+// chunk is loaded into registers (kSlots chunks in flight or waiting per wave) and copied
+// into its ring slot once every compute wave is past the chunk that used the slot before,
+// so HBM keeps streaming while the ring is full and the compute waves wait for a hand-off.
+// The loads are unconditional (past the end they re-read the first line of the weights), so
+// every chunk issues exactly 5 loads and the compiler's vmcnt waits before each copy leave
+// the younger kSlots - 1 chunks in flight.
+__device__ __forceinline__ void run_loader(const StepArgs& a, const Plan& P, float* ring, Ctl& ctl, int lw, int lane) {
+    const float* __restrict__ W = static_cast<const float*>(a.w);
+    const int total = a.layers * P.layer_chunks + P.hn;
+    const int owned = total > lw ? (total - lw + kLW - 1) / kLW : 0;
+    bool failed = false;
+    int cl = P.layer_chunks > 0 ? 0 : a.layers, cr = lw;  // (layer, chunk in layer) of the next chunk to load
+    auto norm = [&]() {
+        while (cl < a.layers && cr >= P.layer_chunks) {
+            cr -= P.layer_chunks;
+            ++cl;
+        }
+    };
+    norm();
+    typedef float v4f __attribute__((ext_vector_type(4)));  // plain vector type: the slots stay in registers
+    v4f slot[kSlots][kLines];
+    auto load = [&](v4f(&d)[kLines], int j) {
+        const float* src[kLines];
+        if (j < owned) {
+            chunk_src(a, P, W, cl, cr, lane, src);
+            cr += kLW;
+            norm();
+        } else {
+#pragma unroll
+            for (int k = 0; k < kLines; ++k) src[k] = W + lane * 4;
+        }
+#pragma unroll
+        for (int k = 0; k < kLines; ++k) d[k] = *reinterpret_cast<const v4f*>(src[k]);
+    };
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) load(slot[s], s);
+    uint32_t lim = kRing;  // chunks below lim may be written: min(need) + kRing
+    for (int j0 = 0; j0 < owned; j0 += kSlots) {
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            const int j = j0 + s;
+            if (j < owned) {
+                const uint32_t c = static_cast<uint32_t>(lw + kLW * j);
+                unsigned spins = 0;
+                while (c >= lim) {
+                    uint32_t m = lds_ld(&ctl.need[0]);
+#pragma unroll
+                    for (int i = 1; i < kCW; ++i) m = min(m, lds_ld(&ctl.need[i]));
+                    lim = m + kRing;
+                    if (c < lim) break;
+                    if (failed || ++spins > kLdsSpinLimit) {
+                        if (!failed) atomicOr(a.err, 1u);
+                        failed = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                float* dst = ring + (c % kRing) * kChunkF + lane * 4;
+#pragma unroll
+                for (int k = 0; k < kLines; ++k) *reinterpret_cast<v4f*>(dst + k * 256) = slot[s][k];
+                if (lane == 0) lds_st(&ctl.done[lw], c + 1);
+            }
+            load(slot[s], j + kSlots);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ compute waves
+
+// Wait until chunk c is in the ring (need[] unchanged).
+__device__ __forceinline__ const float* wait_chunk(Ctl& ctl, const float* ring, int c, uint32_t* err, bool& failed) {
+    unsigned spins = 0;
+    while (lds_ld(&ctl.done[c % kLW]) <= static_cast<uint32_t>(c)) {
+        if (failed || ++spins > kLdsSpinLimit) {
+            if (!failed) atomicOr(err, 1u);
+            failed = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return ring + (c % kRing) * kChunkF;
+}
+__device__ __forceinline__ void release_to(Ctl& ctl, int c, int wave) {
+    if ((threadIdx.x & 63) == 0) lds_st(&ctl.need[wave], static_cast<uint32_t>(c));
+}
+
+// acc += dot(chunk, x) for one 1280-float chunk, in the multi-kernel GEMV's order: lane l
+// takes 16-byte pieces j*64 + l, j ascending, components x, y, z, w.
+__device__ __forceinline__ float dot_chunk(const float* ch, const float* xs, int lane, float acc) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xs + (j * 64 + lane) * 4);
+        const float4 w4 = *reinterpret_cast<const float4*>(ch + (j * 64 + lane) * 4);
+        acc = __builtin_fmaf(w4.x, x4.x, acc);
+        acc = __builtin_fmaf(w4.y, x4.y, acc);
+        acc = __builtin_fmaf(w4.z, x4.z, acc);
+        acc = __builtin_fmaf(w4.w, x4.w, acc);
+    }
+    return acc;
+}
+
+// One group of a wave's rows of a 1280-wide GEMV slice: rows k0 + 4 t (t = 0..3, those
+// below cnt), row k in ring chunk c0 + k.  The four dot products run interleaved and are
+// reduced together (wave_sum4): row k0 + 4 t ends in lanes 0-15, 32-47, 16-31, 48-63 for
+// t = 0, 1, 2, 3.  The group's chunks span 13 < kRing, so holding need at the first one while
+// waiting for the others cannot stall the loaders.
+__device__ __forceinline__ float rows4(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const float* xs, int wave, int lane,
+                                       uint32_t* err, bool& failed) {
+    release_to(ctl, c0 + k0, wave);
+    const float* ch[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int k = k0 + 4 * t;
+        ch[t] = k < cnt ? wait_chunk(ctl, ring, c0 + k, err, failed) : ch[0];  // absent rows re-read row k0
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xs + (j * 64 + lane) * 4);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float4 w4 = *reinterpret_cast<const float4*>(ch[t] + (j * 64 + lane) * 4);
+            acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
+            acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
+            acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
+            acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
+        }
+    }
+    return wave_sum4(acc[0], acc[1], acc[2], acc[3]);
+}
+
+// Runs a wave's rows k = wave + 4 i (< cnt) of a 1280-wide GEMV slice whose row k sits in
+// ring chunk c0 + k, four rows per reduction, and calls out(k, bias, sum) in the lane that
+// holds row k's sum.  Groups g < NG take their bias from `bias`, later ones from bias_mem.
+template <int NG, class Out>
+__device__ __forceinline__ void gemv_rows(Ctl& ctl, const float* ring, int c0, int cnt, const float* xs, const LaneBias<NG, false>& bias,
+                                          const float* __restrict__ bias_mem, int wave, int lane, uint32_t* err, bool& failed, Out out) {
+    const int t = row_of_lane4(lane);
+    const bool holder = (lane & 15) == 0;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int k0 = wave + 16 * g;
+        if (k0 < cnt) {
+            const float v = rows4(ctl, ring, c0, k0, cnt, xs, wave, lane, err, failed);
+            const int k = k0 + 4 * t;
+            if (holder && k < cnt) out(k, bias.v[g], v);
+        }
+    }
+    for (int k0 = wave + 16 * NG; k0 < cnt; k0 += 16) {
+        const float v = rows4(ctl, ring, c0, k0, cnt, xs, wave, lane, err, failed);
+        const int k = k0 + 4 * t;
+        if (holder && k < cnt) out(k, bias_mem[k], v);
+    }
+}
+
+// Two 5120-wide rows (mlp.c_proj) k0, k0 + 4 (the second if below cnt), row k in ring chunks
+// c0 + 4 k + m, m = 0..3, reduced together (wave_sum2: lanes 0 and 32).  A pair's chunks
+// span 20 < kRing.
+__device__ __forceinline__ float rows2_wide(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const float* xs, int wave, int lane,
+                                            uint32_t* err, bool& failed) {
+    const bool two = k0 + kCW < cnt;
+    release_to(ctl, c0 + 4 * k0, wave);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 1
+    for (int m = 0; m < 4; ++m) {
+        const float* c_0 = wait_chunk(ctl, ring, c0 + 4 * k0 + m, err, failed);
+        const float* c_1 = two ? wait_chunk(ctl, ring, c0 + 4 * (k0 + kCW) + m, err, failed) : c_0;
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const float4 x4 = *reinterpret_cast<const float4*>(xs + ((5 * m + j) * 64 + lane) * 4);
+            const float4 w0 = *reinterpret_cast<const float4*>(c_0 + (j * 64 + lane) * 4);
+            const float4 w1 = *reinterpret_cast<const float4*>(c_1 + (j * 64 + lane) * 4);
+            a0 = __builtin_fmaf(w0.x, x4.x, a0);
+            a0 = __builtin_fmaf(w0.y, x4.y, a0);
+            a0 = __builtin_fmaf(w0.z, x4.z, a0);
+            a0 = __builtin_fmaf(w0.w, x4.w, a0);
+            a1 = __builtin_fmaf(w1.x, x4.x, a1);
+            a1 = __builtin_fmaf(w1.y, x4.y, a1);
+            a1 = __builtin_fmaf(w1.z, x4.z, a1);
+            a1 = __builtin_fmaf(w1.w, x4.w, a1);
+        }
+    }
+    return wave_sum2(a0, a1);
+}
+template <int NG, class Out>
+__device__ __forceinline__ void gemv_rows_wide(Ctl& ctl, const float* ring, int c0, int cnt, const float* xs, const LaneBias<NG, true>& bias,
+                                               const float* __restrict__ bias_mem, int wave, int lane, uint32_t* err, bool& failed,
+                                               Out out) {
+    const int t = lane >> 5;
+    const bool holder = (lane & 31) == 0;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int k0 = wave + 8 * g;
+        if (k0 < cnt) {
+            const float v = rows2_wide(ctl, ring, c0, k0, cnt, xs, wave, lane, err, failed);
+            const int k = k0 + 4 * t;
+            if (holder && k < cnt) out(k, bias.v[g], v);
+        }
+    }
+    for (int k0 = wave + 8 * NG; k0 < cnt; k0 += 8) {
+        const float v = rows2_wide(ctl, ring, c0, k0, cnt, xs, wave, lane, err, failed);
+        const int k = k0 + 4 * t;
+        if (holder && k < cnt) out(k, bias_mem[k], v);
+    }
+}
+
+// Row groups per compute wave whose biases are prefetched, per phase: all of them for the
+// slices of a 256-CU grid (15, 5, 20, 5 and 33 rows per workgroup).
+constexpr int kGQkv = 1, kGProj = 1, kGFc = 2, kGFc2 = 1, kGHead = 3;
+
 __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
+    __shared__ float ring[kRing * kChunkF];
+    __shared__ Ctl ctl;
     __shared__ Smem sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const SeqState st = *a.state;
     if (!st.active) return;
+    if (tid < kLW) ctl.done[tid] = 0;
+    if (tid < kCW) ctl.need[tid] = 0;
+    if (tid == 0) ctl.bar = 0;
+    __syncthreads();  // the only barrier of the whole workgroup; roles split below
+
+    Plan P;
+    P.init(st.n, a.splits);
+    const int total_chunks = a.layers * P.layer_chunks + P.hn;
+
+    // ================================================================ loaders
+    if (wave >= kCW) {
+        run_loader(a, P, ring, ctl, __builtin_amdgcn_readfirstlane(wave - kCW), lane);
+        return;
+    }
+
+    // ================================================================ compute waves
     bool failed = false;
-    const uint32_t n = st.n;
-    const int L = static_cast<int>(n) + 1;
-    const int S = live_splits_dev(L, a.splits);
-    const int G = static_cast<int>(gridDim.x);
-    const WT* __restrict__ W = static_cast<const WT*>(a.w);
+    uint32_t gen = 0;
     uint64_t* __restrict__ X = a.xch;
     const uint32_t e0 = a.epoch;
     auto ep = [&](int l, uint32_t kind) { return e0 + 8u * static_cast<uint32_t>(l) + kind; };
+    const uint32_t n = P.n;
 
-#pragma clang loop unroll(disable)
     for (int l = 0; l < a.layers; ++l) {
         const float* __restrict__ par = a.params + static_cast<size_t>(l) * kParLayer;
-        const WT* __restrict__ wl = W + static_cast<size_t>(l) * a.layer_stride;
         const size_t kvl = static_cast<size_t>(l) * a.kv_layer_stride;
+        const int cb = l * P.layer_chunks;  // first chunk of this layer
 
         // ------------------------------------------------ LN1 + c_attn (+ K/V append)
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            Rows<WT, kWidth / 256, kRQkv> R;
-            R.load(wl, kQkv, wave, lane);
-            float hv[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-            if (tid < 256) {
-                if (l == 0) {
-                    // h = mel_emb[token] + mel_pos[position] (gpt.cpp:79-85, kernels.metal:1310-1324)
+            release_to(ctl, cb, wave);
+            // input loads in flight while this wave's c_attn rows move from the ring to registers
+            int idx[5];
+            bool use[5];
 #pragma unroll
-                    for (int i = 0; i < 5; ++i) {
-                        const int c = tid + 256 * i;
-                        hv[i] = a.mel_emb[static_cast<size_t>(st.token) * kWidth + c] + a.mel_pos[static_cast<size_t>(st.position) * kWidth + c];
-                    }
-                } else {
-                    int idx[5];
-                    bool use[5];
+            for (int i = 0; i < 5; ++i) {
+                idx[i] = kXh + tid + 256 * i;
+                use[i] = l > 0;
+            }
+            XRead<5> xr;
+            xr.issue(X, idx, use, ep(l, kEpXh));
+            LnPar ln;
+            ln.load(par + kParLn1W, par + kParLn1B, tid);
+            LaneBias<kGQkv, false> bias;
+            bias.load(par + kParQkvB + P.q0, P.qn, wave, lane);
+            float hv[5];
+            if (l == 0) {
+                // h = mel_emb[token] + mel_pos[position] (gpt.cpp:79-85, kernels.metal:1310-1324)
 #pragma unroll
-                    for (int i = 0; i < 5; ++i) {
-                        idx[i] = kXh + tid + 256 * i;
-                        use[i] = true;
-                    }
-                    xread<5>(X, idx, use, ep(l, kEpXh), hv, a.err, failed);
+                for (int i = 0; i < 5; ++i) {
+                    const int c = tid + 256 * i;
+                    hv[i] = a.mel_emb[static_cast<size_t>(st.token) * kWidth + c] + a.mel_pos[static_cast<size_t>(st.position) * kWidth + c];
                 }
-#pragma unroll
-                for (int i = 0; i < 5; ++i) sm.hraw[tid + 256 * i] = hv[i];
+            } else {
+                xr.wait(X, idx, ep(l, kEpXh), hv, a.err, failed);
             }
-            ln256(hv, par + kParLn1W, par + kParLn1B, sm.red, tid);
-            if (tid < 256) {
 #pragma unroll
-                for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
-            }
-            __syncthreads();
-            float acc[kRQkv];
-            R.dot(sm.xs, acc, wave, lane);
+            for (int i = 0; i < 5; ++i) sm.hraw[tid + 256 * i] = hv[i];
+            ln256(hv, ln.g, ln.b, sm.red, tid, ctl, gen, a.err, failed);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
+            cbar(ctl, gen, a.err, failed);
             const uint32_t e = ep(l, kEpQkv);
-#pragma unroll
-            for (int r = 0; r < kRQkv; ++r) {
-                const int lr = wave + kSW * r;
-                if (lr >= R.cnt || lane != 0) continue;
-                const int row = R.r0 + lr;
-                const float v = acc[r] + par[kParQkvB + row];
+            auto out = [&](int k, float b, float acc) {  // called by the lane holding row k's sum
+                const int row = P.q0 + k;
+                const float v = acc + b;
                 xst(X + kXqkv + row, e, v);
                 if (row >= kWidth) {
                     const int rr = row - kWidth;
@@ -274,60 +643,69 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                     const int c = is_v ? rr - kWidth : rr;
                     a.kv[kvl + (is_v ? a.kv_v_off : 0) + (static_cast<size_t>(c >> 6) * a.kv_cap + n) * kHeadDim + (c & 63)] = v;
                 }
-            }
+            };
+            gemv_rows(ctl, ring, cb, P.qn, sm.xs, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
         }
 
         // ------------------------------------------------ split-KV attention tiles
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            const int ntiles = kHeads * S;
-            const int quarter = tid >> 8, t = tid & 255, g = t >> 4, sub = t & 15, qw = (t >> 6);
-            const int chunk = (L + S - 1) / S;
-            const int rounds = (ntiles + kSH * G - 1) / (kSH * G);
+            const int g = tid >> 4, sub = tid & 15;
             const uint32_t eq = ep(l, kEpQkv), epart = ep(l, kEpPart);
-#pragma clang loop unroll(disable)
-            for (int rd = 0; rd < rounds; ++rd) {
-                const int tile = static_cast<int>(blockIdx.x) + G * (kSH * rd + quarter);
-                const bool act = tile < ntiles;
-                const int h = act ? tile % kHeads : 0, s = act ? tile / kHeads : 0;
-                const int p0 = s * chunk, p1 = min(L, p0 + chunk);
+            int ca = cb + P.o_att;  // first chunk of the current tile
+            release_to(ctl, ca, wave);
+            for (int rd = 0; rd < P.rounds; ++rd) {
+                int h = 0, s = 0, t0 = 0, R = 0;
+                const bool act = P.tile(rd, h, s, t0, R);
+                const int p1 = act ? min(P.L, t0 + P.chunk_rows) : 0;
+                const int kc = act ? Plan::kv_chunks(R) : 0;
                 // 8 arithmetic slots as attention_kernel; a tile has <= 64 rows here (KV capacity
                 // <= 4096, checked on the host), so only slots 0..3 can hold a row and slots
                 // 4..7 stay constant zeros (-inf scores) exactly as in the multi-kernel path.
                 constexpr int PER = kAttnMaxChunk / 16;
                 constexpr int PERL = 4;
                 float4 k4[PER], v4[PER];
-                // cached rows first (no dependency on this step), the new row and q after
 #pragma unroll
                 for (int i = 0; i < PER; ++i) {
-                    const int p = p0 + g + 16 * i;
-                    if (i < PERL && act && p < p1 && p != static_cast<int>(n)) {
-                        const size_t base = kvl + (static_cast<size_t>(h) * a.kv_cap + p) * kHeadDim + sub * 4;
-                        k4[i] = *reinterpret_cast<const float4*>(a.kv + base);
-                        v4[i] = *reinterpret_cast<const float4*>(a.kv + base + a.kv_v_off);
-                    } else {
-                        k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                        v4[i] = k4[i];
+                    k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    v4[i] = k4[i];
+                }
+                // q and, in the tile holding it, the row appended by this step (row n): loads in
+                // flight while the cached rows move from the ring to registers
+                const int dn = static_cast<int>(n) - t0 - g;
+                const int i_new = (act && static_cast<int>(n) < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < PERL) ? (dn >> 4) : -1;
+                int idx[12];
+                bool use[12];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    idx[k] = kXqkv + h * kHeadDim + sub * 4 + k;
+                    idx[4 + k] = kXqkv + kWidth + h * kHeadDim + sub * 4 + k;
+                    idx[8 + k] = kXqkv + 2 * kWidth + h * kHeadDim + sub * 4 + k;
+                    use[k] = act;
+                    use[4 + k] = use[8 + k] = i_new >= 0;
+                }
+                XRead<12> xr;
+                xr.issue(X, idx, use, eq);
+                // cached rows from the ring; need stays at the tile's first chunk until its rows
+                // are in registers
+                for (int j = 0; j < 2 * kc; ++j) (void)wait_chunk(ctl, ring, ca + j, a.err, failed);
+#pragma unroll
+                for (int i = 0; i < PERL; ++i) {
+                    const int r = g + 16 * i;  // tile-local row
+                    if (act && r < R) {
+                        const float* kch = ring + ((ca + r / kKvRowsPerChunk) % kRing) * kChunkF;
+                        const float* vch = ring + ((ca + kc + r / kKvRowsPerChunk) % kRing) * kChunkF;
+                        const int off = (r % kKvRowsPerChunk) * kHeadDim + sub * 4;
+                        k4[i] = *reinterpret_cast<const float4*>(kch + off);
+                        v4[i] = *reinterpret_cast<const float4*>(vch + off);
                     }
                 }
-                // q and, in the tile holding it, the row appended by this step (row n): one
-                // gather of tagged values each; row n sits at slot i_new of thread group g.
-                const int dn = static_cast<int>(n) - p0 - g;
-                const int i_new = (act && static_cast<int>(n) < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < PERL) ? (dn >> 4) : -1;
-                float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                ca += 2 * kc;
+                release_to(ctl, ca, wave);  // this tile's chunks are in registers now
+                float4 q4;
                 {
-                    int idx[12];
-                    bool use[12];
                     float qv[12];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        idx[k] = kXqkv + h * kHeadDim + sub * 4 + k;
-                        idx[4 + k] = kXqkv + kWidth + h * kHeadDim + sub * 4 + k;
-                        idx[8 + k] = kXqkv + 2 * kWidth + h * kHeadDim + sub * 4 + k;
-                        use[k] = act;
-                        use[4 + k] = use[8 + k] = i_new >= 0;
-                    }
-                    xread<12>(X, idx, use, eq, qv, a.err, failed);
+                    xr.wait(X, idx, eq, qv, a.err, failed);
                     q4 = make_float4(qv[0], qv[1], qv[2], qv[3]);
                     const float4 kn = make_float4(qv[4], qv[5], qv[6], qv[7]);
                     const float4 vn = make_float4(qv[8], qv[9], qv[10], qv[11]);
@@ -348,23 +726,20 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                     d = __builtin_fmaf(q4.y, k4[i].y, d);
                     d = __builtin_fmaf(q4.z, k4[i].z, d);
                     d = __builtin_fmaf(q4.w, k4[i].w, d);
-                    d += __shfl_xor(d, 1, 64);
-                    d += __shfl_xor(d, 2, 64);
-                    d += __shfl_xor(d, 4, 64);
-                    d += __shfl_xor(d, 8, 64);
-                    const bool valid = i < PERL && act && p0 + g + 16 * i < p1;
+                    d = sum16_up(d);
+                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
                     sc[i] = valid ? d * 0.125f : -INFINITY;
                     mloc = fmaxf(mloc, sc[i]);
                 }
                 const float wm = wave_max(mloc);
-                if (lane == 0) sm.redm[quarter][qw] = wm;
-                __syncthreads();
-                const float M = fmaxf(fmaxf(sm.redm[quarter][0], sm.redm[quarter][1]), fmaxf(sm.redm[quarter][2], sm.redm[quarter][3]));
+                if (lane == 0) sm.redm[wave] = wm;
+                cbar(ctl, gen, a.err, failed);
+                const float M = fmaxf(fmaxf(sm.redm[0], sm.redm[1]), fmaxf(sm.redm[2], sm.redm[3]));
                 float lsum = 0.0f;
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                 for (int i = 0; i < PER; ++i) {
-                    const bool valid = i < PERL && act && p0 + g + 16 * i < p1;
+                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
                     const float e = valid ? expf(sc[i] - M) : 0.0f;
                     lsum += e;
                     acc.x = __builtin_fmaf(e, v4[i].x, acc.x);
@@ -373,243 +748,225 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                     acc.w = __builtin_fmaf(e, v4[i].w, acc.w);
                 }
                 const float ws = wave_sum(sub == 0 ? lsum : 0.0f);
-                if (lane == 0) sm.reds[quarter][qw] = ws;
-                sm.accs[quarter][g][sub * 4 + 0] = acc.x;
-                sm.accs[quarter][g][sub * 4 + 1] = acc.y;
-                sm.accs[quarter][g][sub * 4 + 2] = acc.z;
-                sm.accs[quarter][g][sub * 4 + 3] = acc.w;
-                __syncthreads();
-                if (act && t < kHeadDim) {
+                if (lane == 0) sm.reds[wave] = ws;
+                sm.accs[g][sub * 4 + 0] = acc.x;
+                sm.accs[g][sub * 4 + 1] = acc.y;
+                sm.accs[g][sub * 4 + 2] = acc.z;
+                sm.accs[g][sub * 4 + 3] = acc.w;
+                cbar(ctl, gen, a.err, failed);
+                if (act && tid < kHeadDim) {
                     float tot = 0.0f;
 #pragma unroll
-                    for (int gg = 0; gg < 16; ++gg) tot += sm.accs[quarter][gg][t];
+                    for (int gg = 0; gg < 16; ++gg) tot += sm.accs[gg][tid];
                     uint64_t* part = X + kXpart + (static_cast<size_t>(h) * kAttnMaxSplits + s) * 68;
-                    xst(part + 4 + t, epart, tot);
-                    if (t == 0) {
+                    xst(part + 4 + tid, epart, tot);
+                    if (tid == 0) {
                         xst(part + 0, epart, M);
-                        xst(part + 1, epart,
-                            ((sm.reds[quarter][0] + sm.reds[quarter][1]) + sm.reds[quarter][2]) + sm.reds[quarter][3]);
+                        xst(part + 1, epart, ((sm.reds[0] + sm.reds[1]) + sm.reds[2]) + sm.reds[3]);
                     }
                 }
-                __syncthreads();  // accs/redm are reused by the next round
+                cbar(ctl, gen, a.err, failed);  // redm/reds/accs are reused by the next round
             }
+            release_to(ctl, cb + P.o_proj, wave);
         }
 
         // ------------------------------------------------ merge of the splits of head h (workgroup h)
-        if (static_cast<int>(blockIdx.x) < kHeads) {
+        if (P.b < kHeads) {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            // All threads gather the S partial records (m, l, acc[64]) of head h into LDS,
-            // then waves 0-3 merge them in the order of attention_merge_kernel (decode.hip).
-            const int h = blockIdx.x;
+            // The compute threads gather the S partial records (m, l, acc[64]) of head h into
+            // LDS, then merge them in the order of attention_merge_kernel (decode.hip).
+            const int h = P.b;
             const uint64_t* pb = X + kXpart + static_cast<size_t>(h) * kAttnMaxSplits * 68;
             constexpr int kRec = 2 + kHeadDim;  // values used per record
-            constexpr int NPT = (kAttnMaxSplits * kRec + kST - 1) / kST;
+            constexpr int NPT = (kAttnMaxSplits * kRec + kCT - 1) / kCT;
             {
                 int idx[NPT];
                 bool use[NPT];
                 float v[NPT];
 #pragma unroll
                 for (int i = 0; i < NPT; ++i) {
-                    const int q = tid + kST * i;  // record q / kRec, field q % kRec
+                    const int q = tid + kCT * i;  // record q / kRec, field q % kRec
                     const int k = q / kRec, f = q % kRec;
                     idx[i] = k * 68 + (f < 2 ? f : f + 2);
-                    use[i] = k < S;
+                    use[i] = k < P.S;
                 }
                 xread<NPT>(pb, idx, use, ep(l, kEpPart), v, a.err, failed);
 #pragma unroll
                 for (int i = 0; i < NPT; ++i) {
-                    const int q = tid + kST * i;
+                    const int q = tid + kCT * i;
                     if (use[i]) sm.mpart[q / kRec][q % kRec] = v[i];
                 }
             }
-            __syncthreads();
-            const bool act = tid < 256;
-            constexpr int PW = kAttnMaxSplits / 4;
-            float mk[PW], lk[PW], ak[PW];
-#pragma unroll
-            for (int i = 0; i < PW; ++i) {
-                const int k = wave + 4 * i;
-                const bool ok = act && k < S;
-                mk[i] = ok ? sm.mpart[k][0] : -INFINITY;
-                lk[i] = ok ? sm.mpart[k][1] : 0.0f;
-                ak[i] = ok ? sm.mpart[k][2 + lane] : 0.0f;
-            }
+            cbar(ctl, gen, a.err, failed);
+            // wave w takes splits w, w+4, ... (attention_merge_kernel's order), straight from LDS
             float m = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < PW; ++i) m = fmaxf(m, mk[i]);
-            if (act && lane == 0) sm.mwm[wave] = m;
-            __syncthreads();
+            for (int k = wave; k < P.S; k += 4) m = fmaxf(m, sm.mpart[k][0]);
+            if (lane == 0) sm.mwm[wave] = m;
+            cbar(ctl, gen, a.err, failed);
             const float mg = fmaxf(fmaxf(sm.mwm[0], sm.mwm[1]), fmaxf(sm.mwm[2], sm.mwm[3]));
             float den = 0.0f, num = 0.0f;
-#pragma unroll
-            for (int i = 0; i < PW; ++i) {
-                const float wgt = mk[i] == -INFINITY ? 0.0f : expf(mk[i] - mg);
-                den = __builtin_fmaf(lk[i], wgt, den);
-                num = __builtin_fmaf(ak[i], wgt, num);
+            for (int k = wave; k < P.S; k += 4) {
+                const float mk = sm.mpart[k][0];
+                const float wgt = mk == -INFINITY ? 0.0f : expf(mk - mg);
+                den = __builtin_fmaf(sm.mpart[k][1], wgt, den);
+                num = __builtin_fmaf(sm.mpart[k][2 + lane], wgt, num);
             }
-            if (act) {
-                sm.mwnum[wave][lane] = num;
-                if (lane == 0) sm.mwden[wave] = den;
-            }
-            __syncthreads();
+            sm.mwnum[wave][lane] = num;
+            if (lane == 0) sm.mwden[wave] = den;
+            cbar(ctl, gen, a.err, failed);
             if (wave == 0) {
                 const float d = ((sm.mwden[0] + sm.mwden[1]) + sm.mwden[2]) + sm.mwden[3];
                 const float nn = ((sm.mwnum[0][lane] + sm.mwnum[1][lane]) + sm.mwnum[2][lane]) + sm.mwnum[3][lane];
                 xst(X + kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
             }
+            cbar(ctl, gen, a.err, failed);  // mpart aliases xs, written below
         }
 
         // ------------------------------------------------ attn.c_proj + residual
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            Rows<WT, kWidth / 256, kRProj> R;
-            R.load(wl + static_cast<size_t>(kQkv) * kWidth, kWidth, wave, lane);
+            const int cp = cb + P.o_proj;
+            int idx[5];
+            bool use[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                idx[i] = kXattn + tid + 256 * i;
+                use[i] = true;
+            }
+            XRead<5> xr;
+            xr.issue(X, idx, use, ep(l, kEpAttn));
+            LaneBias<kGProj, false> bias;
+            bias.load(par + kParProjB + P.p0, P.pn, wave, lane);
             {
-                constexpr int NA = (kWidth + kST - 1) / kST;
-                int idx[NA];
-                bool use[NA];
-                float v[NA];
+                float v[5];
+                xr.wait(X, idx, ep(l, kEpAttn), v, a.err, failed);
 #pragma unroll
-                for (int i = 0; i < NA; ++i) {
-                    idx[i] = kXattn + tid + kST * i;
-                    use[i] = tid + kST * i < kWidth;
-                }
-                xread<NA>(X, idx, use, ep(l, kEpAttn), v, a.err, failed);
-#pragma unroll
-                for (int i = 0; i < NA; ++i)
-                    if (use[i]) sm.xs[tid + kST * i] = v[i];
+                for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = v[i];
             }
-            __syncthreads();
-            float acc[kRProj];
-            R.dot(sm.xs, acc, wave, lane);
+            cbar(ctl, gen, a.err, failed);
             const uint32_t e = ep(l, kEpHmid);
-#pragma unroll
-            for (int r = 0; r < kRProj; ++r) {
-                const int lr = wave + kSW * r;
-                if (lr >= R.cnt || lane != 0) continue;
-                const int row = R.r0 + lr;
-                xst(X + kXhmid + row, e, sm.hraw[row] + (acc[r] + par[kParProjB + row]));
-            }
+            auto out = [&](int k, float b, float acc) {
+                const int row = P.p0 + k;
+                xst(X + kXhmid + row, e, sm.hraw[row] + (acc + b));
+            };
+            gemv_rows(ctl, ring, cp, P.pn, sm.xs, bias, par + kParProjB + P.p0, wave, lane, a.err, failed, out);
+            release_to(ctl, cb + P.o_fc, wave);
         }
 
         // ------------------------------------------------ LN2 + c_fc + GELU
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            Rows<WT, kWidth / 256, kRFc> R;
-            R.load(wl + static_cast<size_t>(kQkv + kWidth) * kWidth, kFfn, wave, lane);
-            float hv[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-            if (tid < 256) {
-                int idx[5];
-                bool use[5];
+            const int cf = cb + P.o_fc;
+            int idx[5];
+            bool use[5];
 #pragma unroll
-                for (int i = 0; i < 5; ++i) {
-                    idx[i] = kXhmid + tid + 256 * i;
-                    use[i] = true;
-                }
-                xread<5>(X, idx, use, ep(l, kEpHmid), hv, a.err, failed);
-#pragma unroll
-                for (int i = 0; i < 5; ++i) sm.mraw[tid + 256 * i] = hv[i];
+            for (int i = 0; i < 5; ++i) {
+                idx[i] = kXhmid + tid + 256 * i;
+                use[i] = true;
             }
-            ln256(hv, par + kParLn2W, par + kParLn2B, sm.red, tid);
-            if (tid < 256) {
+            XRead<5> xr;
+            xr.issue(X, idx, use, ep(l, kEpHmid));
+            LnPar ln;
+            ln.load(par + kParLn2W, par + kParLn2B, tid);
+            LaneBias<kGFc, false> bias;
+            bias.load(par + kParFcB + P.f0, P.fn, wave, lane);
+            float hv[5];
+            xr.wait(X, idx, ep(l, kEpHmid), hv, a.err, failed);
 #pragma unroll
-                for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
-            }
-            __syncthreads();
-            float acc[kRFc];
-            R.dot(sm.xs, acc, wave, lane);
+            for (int i = 0; i < 5; ++i) sm.mraw[tid + 256 * i] = hv[i];
+            cbar(ctl, gen, a.err, failed);  // every wave is past its c_proj reads of xs
+            ln256(hv, ln.g, ln.b, sm.red, tid, ctl, gen, a.err, failed);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
+            cbar(ctl, gen, a.err, failed);
             const uint32_t e = ep(l, kEpFf);
-#pragma unroll
-            for (int r = 0; r < kRFc; ++r) {
-                const int lr = wave + kSW * r;
-                if (lr >= R.cnt || lane != 0) continue;
-                const int row = R.r0 + lr;
-                xst(X + kXff + row, e, gelu_f(acc[r] + par[kParFcB + row]));
-            }
+            auto out = [&](int k, float b, float acc) {
+                const int row = P.f0 + k;
+                xst(X + kXff + row, e, gelu_f(acc + b));
+            };
+            gemv_rows(ctl, ring, cf, P.fn, sm.xs, bias, par + kParFcB + P.f0, wave, lane, a.err, failed, out);
+            release_to(ctl, cb + P.o_fc2, wave);
         }
 
         // ------------------------------------------------ mlp.c_proj + residual -> next h
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            Rows<WT, kFfn / 256, kRFc2> R;
-            R.load(wl + static_cast<size_t>(kQkv + kWidth + kFfn) * kWidth, kWidth, wave, lane);
+            const int cg = cb + P.o_fc2;
+            constexpr int NF = kFfn / kCT;
+            int idx[NF];
+            bool use[NF];
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                idx[i] = kXff + tid + kCT * i;
+                use[i] = true;
+            }
+            XRead<NF> xr;
+            xr.issue(X, idx, use, ep(l, kEpFf));
+            LaneBias<kGFc2, true> bias;
+            bias.load(par + kParFc2B + P.g0, P.gn, wave, lane);
+            cbar(ctl, gen, a.err, failed);  // every wave is past its c_fc reads of xs
             {
-                constexpr int NF = kFfn / kST;
-                int idx[NF];
-                bool use[NF];
                 float v[NF];
+                xr.wait(X, idx, ep(l, kEpFf), v, a.err, failed);
 #pragma unroll
-                for (int i = 0; i < NF; ++i) {
-                    idx[i] = kXff + tid + kST * i;
-                    use[i] = true;
-                }
-                xread<NF>(X, idx, use, ep(l, kEpFf), v, a.err, failed);
-#pragma unroll
-                for (int i = 0; i < NF; ++i) sm.xs[tid + kST * i] = v[i];
+                for (int i = 0; i < NF; ++i) sm.xs[tid + kCT * i] = v[i];
             }
-            __syncthreads();
-            float acc[1];
-            R.dot(sm.xs, acc, wave, lane);
-            if (wave < R.cnt && lane == 0) {
-                const int row = R.r0 + wave;
-                xst(X + kXh + row, ep(l + 1, kEpXh), sm.mraw[row] + (acc[0] + par[kParFc2B + row]));
-            }
+            cbar(ctl, gen, a.err, failed);
+            auto out = [&](int k, float b, float acc) {
+                const int row = P.g0 + k;
+                xst(X + kXh + row, ep(l + 1, kEpXh), sm.mraw[row] + (acc + b));
+            };
+            gemv_rows_wide(ctl, ring, cg, P.gn, sm.xs, bias, par + kParFc2B + P.g0, wave, lane, a.err, failed, out);
+            release_to(ctl, (l + 1) * P.layer_chunks, wave);
+            cbar(ctl, gen, a.err, failed);  // every wave is past its reads of xs and mraw
         }
     }
 
     // ---------------------------------------------------- ln_f, final_norm, mel_head
     {
-            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-        Rows<WT, kWidth / 256, kRHead> R;
-        R.load(W + a.off_head, kMelVocab, wave, lane);
-        float hv[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-        if (tid < 256) {
-            int idx[5];
-            bool use[5];
+        const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+        const int chd = a.layers * P.layer_chunks;
+        int idx[5];
+        bool use[5];
 #pragma unroll
-            for (int i = 0; i < 5; ++i) {
-                idx[i] = kXh + tid + 256 * i;
-                use[i] = true;
-            }
-            xread<5>(X, idx, use, ep(a.layers, kEpXh), hv, a.err, failed);
+        for (int i = 0; i < 5; ++i) {
+            idx[i] = kXh + tid + 256 * i;
+            use[i] = true;
         }
-        ln256(hv, a.head + kHeadLnfW, a.head + kHeadLnfB, sm.red, tid);
-        ln256(hv, a.head + kHeadFnW, a.head + kHeadFnB, sm.red, tid);
-        if (tid < 256) {
+        XRead<5> xr;
+        xr.issue(X, idx, use, ep(a.layers, kEpXh));
+        LnPar lf, fn;
+        lf.load(a.head + kHeadLnfW, a.head + kHeadLnfB, tid);
+        fn.load(a.head + kHeadFnW, a.head + kHeadFnB, tid);
+        LaneBias<kGHead, false> bias;
+        bias.load(a.head + kHeadBias + P.h0, P.hn, wave, lane);
+        float hv[5];
+        xr.wait(X, idx, ep(a.layers, kEpXh), hv, a.err, failed);
+        ln256(hv, lf.g, lf.b, sm.red, tid, ctl, gen, a.err, failed);
+        ln256(hv, fn.g, fn.b, sm.red, tid, ctl, gen, a.err, failed);
 #pragma unroll
-            for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
-        }
-        __syncthreads();
-        float acc[kRHead];
-        R.dot(sm.xs, acc, wave, lane);
-#pragma unroll
-        for (int r = 0; r < kRHead; ++r) {
-            const int lr = wave + kSW * r;
-            if (lr >= R.cnt || lane != 0) continue;
-            const int row = R.r0 + lr;
-            a.logits[row] = acc[r] + a.head[kHeadBias + row];
-        }
+        for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
+        cbar(ctl, gen, a.err, failed);
+        auto out = [&](int k, float b, float acc) { a.logits[P.h0 + k] = acc + b; };
+        gemv_rows(ctl, ring, chd, P.hn, sm.xs, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
+        release_to(ctl, total_chunks, wave);
     }
 }
 
 }  // namespace
 
-bool step_fits(int grid) {
-    auto per = [&](int rows) { return (rows + grid - 1) / grid; };
-    return grid > 0 && per(kQkv) <= kSW * kRQkv && per(kWidth) <= kSW * kRProj && per(kFfn) <= kSW * kRFc &&
-           per(kWidth) <= kSW * kRFc2 && per(kMelVocab) <= kSW * kRHead && grid >= kHeads;
-}
+bool step_fits(int grid) { return grid >= kHeads; }
 
-// FP32 weights only: the BF16 instantiation does not fit the register file without
-// spilling, so BF16 decoders keep the multi-kernel path.
+// FP32 weights only (the loaders copy 16-byte FP32 lines); BF16 decoders keep the
+// multi-kernel path.
 hipError_t step_occupancy(bool bf16, int* blocks_per_cu) {
     if (bf16) return hipErrorInvalidValue;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, step_kernel<float>, kST, 0);
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, step_kernel, kST, 0);
 }
 
 hipError_t launch_step(const StepArgs& a, int grid, bool bf16, hipStream_t s) {
     if (bf16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(step_kernel<float>, dim3(grid), dim3(kST), 0, s, a);
+    hipLaunchKernelGGL(step_kernel, dim3(grid), dim3(kST), 0, s, a);
     return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <thread>
@@ -83,6 +84,30 @@ struct Snapshot {
     DevBuf<float> kv;
 };
 
+// A persistent step grid takes one workgroup slot on every CU and needs all of its
+// workgroups resident together.  Two such grids running at once on one GPU (decoders of
+// this process on different streams) could each hold CUs the other is waiting for, so
+// the launches on a device are chained: each waits for the previous one, whichever decoder
+// made it.  The chain is process-wide and never freed.
+hipError_t launch_step_serialized(const StepArgs& a, int grid, bool bf16, int dev, hipStream_t s) {
+    static std::mutex mu;
+    static std::unordered_map<int, hipEvent_t> last;  // device -> recorded after its latest step launch
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = last.find(dev);
+    if (it == last.end()) {
+        hipEvent_t e = nullptr;
+        const hipError_t err = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+        if (err != hipSuccess) return err;
+        it = last.emplace(dev, e).first;
+    } else {
+        const hipError_t err = hipStreamWaitEvent(s, it->second, 0);
+        if (err != hipSuccess) return err;
+    }
+    const hipError_t err = launch_step(a, grid, bf16, s);
+    if (err != hipSuccess) return err;
+    return hipEventRecord(it->second, s);
+}
+
 }  // namespace
 
 struct Engine {
@@ -123,10 +148,11 @@ struct Engine {
     SeqState* pinned_state = nullptr;
     int splits = 16;
     bool use_graphs = true;  // ITTS_GPT_GRAPHS=0: launch the same kernels eagerly (profilers)
-    // Persistent single-sequence step (step.hip): one launch per token.  Opt-in with
-    // ITTS_GPT_PERSISTENT=1; otherwise batch 1 uses the multi-kernel graph path.
+    // Persistent single-sequence step (step.hip): one launch per token for batch-1 decode
+    // (bitwise the same logits as the multi-kernel path, which ITTS_GPT_PERSISTENT=0 selects).
     bool step_ok = false;
     int step_grid = 0;
+    int step_dev = 0;
     size_t per_layer = 0;       // weight elements per layer block
     DevBuf<uint64_t> xch;       // tagged exchange slots
     DevBuf<uint32_t> step_err;  // hand-off timeout flag
@@ -308,14 +334,15 @@ struct Engine {
     }
 
     // The persistent step runs when one 512-thread workgroup fits per CU (the grid is one
-    // workgroup per CU, all resident together), the per-CU weight slices fit the kernel's
-    // register tiles (step_fits), weights are FP32 and attention tiles stay <= 64 rows
-    // (cap <= 4096).
+    // workgroup per CU, all resident together), there is a workgroup per attention head
+    // (step_fits: head h's merge runs on workgroup h), weights are FP32 and attention
+    // tiles stay <= 64 rows (cap <= 4096).
     void init_step() {
         const char* pe = std::getenv("ITTS_GPT_PERSISTENT");
-        if (!pe || std::strcmp(pe, "1") != 0 || bf16 || cap > 4096) return;
+        if ((pe && std::strcmp(pe, "0") == 0) || bf16 || cap > 4096) return;
         int dev = 0, cus = 0, occ = 0;
         HIP_CHECK(hipGetDevice(&dev));
+        step_dev = dev;
         HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         HIP_CHECK(step_occupancy(false, &occ));
         if (occ < 1 || !step_fits(cus)) return;
@@ -487,7 +514,7 @@ struct Engine {
     void run_step(int nseq, int nb, bool sampler, bool use_table) {
         if (persistent(nseq, use_table)) {
             timing.decode_path = ITTS_PATH_STEP;
-            HIP_CHECK(launch_step(step_args(), step_grid, bf16, stream));
+            HIP_CHECK(launch_step_serialized(step_args(), step_grid, bf16, step_dev, stream));
             if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
             return;
         }
@@ -952,7 +979,7 @@ struct Engine {
                     enqueue_head(batch, nb);
                     break;
                 case 6:
-                    HIP_CHECK(launch_step(step_args(), step_grid, bf16, stream));
+                    HIP_CHECK(launch_step_serialized(step_args(), step_grid, bf16, step_dev, stream));
                     break;
                 default: {
                     AttnArgs t{};

@@ -147,7 +147,7 @@ __device__ __forceinline__ void lds_st(uint32_t* p, uint32_t v) {
 
 // Ring hand-shake words and the compute-wave barrier counter (an LDS object apart from
 // the ring).
-struct Ctl {
+struct alignas(16) Ctl {
     uint32_t done[kLW];  // loader w: 1 + last chunk index landed (its chunks are w, w+4, ...)
     uint32_t need[kCW];  // compute wave c: first chunk it may still read
     uint32_t bar;        // compute-wave barrier arrivals
@@ -169,34 +169,47 @@ __device__ __forceinline__ void cbar(Ctl& ctl, uint32_t& gen, uint32_t* err, boo
     }
 }
 
-// LayerNorm of one 1280-wide row held by the 256 compute threads (value tid + 256 i), in
-// the order of ln_block<1, 5> (common.h): wave butterfly, then the 4 wave partials in order.
-__device__ __forceinline__ void ln256(float (&v)[5], const float (&g)[5], const float (&be)[5], float* red, int tid, Ctl& ctl,
-                                      uint32_t& gen, uint32_t* err, bool& failed) {
-    const int lane = tid & 63, wave = tid >> 6;
-    float s = 0.0f;
+__device__ __forceinline__ float lane_value(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+// A 1280-wide row in LDS, as the 256 threads of ln_block<1, 5> (common.h) hold it:
+// v[w][i] = row[64 w + lane + 256 i], i.e. thread 64 w + lane's five values.
+__device__ __forceinline__ void ln_layout_load(const float* row, int lane, float (&v)[4][5]) {
 #pragma unroll
-    for (int i = 0; i < 5; ++i) s += v[i];
-    s = wave_sum(s);
-    if (lane == 0) red[wave] = s;
-    cbar(ctl, gen, err, failed);
-    const float mean = (((red[0] + red[1]) + red[2]) + red[3]) / float(kWidth);
-    cbar(ctl, gen, err, failed);
-    s = 0.0f;
+    for (int w = 0; w < 4; ++w)
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const float d = v[i] - mean;
-        s += d * d;
-    }
-    s = wave_sum(s);
-    if (lane == 0) red[wave] = s;
-    cbar(ctl, gen, err, failed);
-    const float var = (((red[0] + red[1]) + red[2]) + red[3]) / float(kWidth);
-    const float inv = 1.0f / sqrtf(var + kLnEps);
-#pragma unroll
-    for (int i = 0; i < 5; ++i) v[i] = (v[i] - mean) * inv * g[i] + be[i];
-    cbar(ctl, gen, err, failed);
+        for (int i = 0; i < 5; ++i) v[w][i] = row[64 * w + lane + 256 * i];
 }
+
+// Mean and 1 / sqrt(var + eps) of that row in ln_block<1, 5>'s order (each thread sums its
+// five values, each wave reduces its threads by butterfly, the four wave sums are added in
+// order), computed by one wave for all four: wave_sum4 reduces the four waves' values with
+// wave_sum's pairings, so every compute wave gets the statistics without a barrier.
+__device__ __forceinline__ void ln_stats(const float (&v)[4][5], float& mean, float& inv) {
+    float s[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        s[w] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) s[w] += v[w][i];
+    }
+    float r = wave_sum4(s[0], s[1], s[2], s[3]);  // waves 0, 1, 2, 3 in lanes 0, 32, 16, 48
+    mean = (((lane_value(r, 0) + lane_value(r, 32)) + lane_value(r, 16)) + lane_value(r, 48)) / float(kWidth);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        s[w] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const float d = v[w][i] - mean;
+            s[w] += d * d;
+        }
+    }
+    r = wave_sum4(s[0], s[1], s[2], s[3]);
+    const float var = (((lane_value(r, 0) + lane_value(r, 32)) + lane_value(r, 16)) + lane_value(r, 48)) / float(kWidth);
+    inv = 1.0f / sqrtf(var + kLnEps);
+}
+// ln_block's per-element step
+__device__ __forceinline__ float ln_apply(float v, float mean, float inv, float g, float b) { return (v - mean) * inv * g + b; }
+
 // gamma/beta of this thread's 5 LayerNorm columns (tid + 256 i), loaded ahead of the input.
 struct LnPar {
     float g[5], b[5];
@@ -208,6 +221,18 @@ struct LnPar {
         }
     }
 };
+// gamma/beta of this lane's 20 columns in the GEMV's lane order (4 (j*64 + lane) .. + 3).
+struct LnParDot {
+    float4 g[5], b[5];
+    __device__ __forceinline__ void load(const float* __restrict__ gp, const float* __restrict__ bp, int lane) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            g[j] = *reinterpret_cast<const float4*>(gp + (j * 64 + lane) * 4);
+            b[j] = *reinterpret_cast<const float4*>(bp + (j * 64 + lane) * 4);
+        }
+    }
+};
+
 // Lane holding row k0 + 4 t's sum after wave_sum4 (rows k0 + 4 t, t = 0..3): lanes 0, 32,
 // 16, 48 for t = 0, 1, 2, 3; for wave_sum2 (rows k0, k0 + 4): lanes 0 and 32.
 __device__ __forceinline__ int row_of_lane4(int lane) { return (lane >> 5) + 2 * ((lane >> 4) & 1); }
@@ -290,16 +315,13 @@ struct Plan {
 
 struct Smem {
     union {
-        float xs[kFfn];                             // phase input (normalised where a LayerNorm precedes the GEMV)
+        float xs[kFfn];                             // GEMV input of attn.c_proj and mlp.c_proj; ln_f output
         float mpart[kAttnMaxSplits][2 + kHeadDim];  // gathered attention partials of one head (merge)
     };
     float hraw[kWidth];  // layer input h (residual of attn.c_proj)
     float mraw[kWidth];  // hmid (residual of mlp.c_proj)
-    float red[4];
     float redm[4], reds[4];
     float accs[16][kHeadDim + 4];
-    float mwm[4], mwden[4];
-    float mwnum[4][kHeadDim];
 };
 
 // ------------------------------------------------------------------ loader waves
@@ -434,6 +456,29 @@ __device__ __forceinline__ const float* wait_chunk(Ctl& ctl, const float* ring, 
     }
     return ring + (c % kRing) * kChunkF;
 }
+// Wait until chunks c .. c + 3 (one per loader) are all in the ring: one 16-byte read of
+// the four done[] words per poll.
+__device__ __forceinline__ void wait_run4(Ctl& ctl, int c, uint32_t* err, bool& failed) {
+    unsigned spins = 0;
+    while (true) {
+        // one ds_read_b128 (volatile: re-read every poll); the ring reads that follow are
+        // issued only after the branch on this value, and LDS serves a wave's reads in order
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 d = *reinterpret_cast<const volatile u32x4*>(ctl.done);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const uint32_t dd[4] = {d.x, d.y, d.z, d.w};
+        bool ok = true;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) ok &= dd[(c + m) % kLW] > static_cast<uint32_t>(c + m);
+        if (ok) break;
+        if (failed || ++spins > kLdsSpinLimit) {
+            if (!failed) atomicOr(err, 1u);
+            failed = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
 __device__ __forceinline__ void release_to(Ctl& ctl, int c, int wave) {
     if ((threadIdx.x & 63) == 0) lds_st(&ctl.need[wave], static_cast<uint32_t>(c));
 }
@@ -453,41 +498,70 @@ __device__ __forceinline__ float dot_chunk(const float* ch, const float* xs, int
     return acc;
 }
 
+// A 1280-wide input vector in registers, in the GEMV's lane order: x[j] = floats
+// 4 (j*64 + lane) .. +3.  Loaded once per phase and reused by every row group.
+struct XRow {
+    float4 x[5];
+    __device__ __forceinline__ void load(const float* xs, int lane) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j) x[j] = *reinterpret_cast<const float4*>(xs + (j * 64 + lane) * 4);
+    }
+};
+
+// x = LayerNorm(row) in the GEMV's lane order, from the raw row in LDS and its statistics.
+__device__ __forceinline__ void ln_to_xrow(const float* row, int lane, float mean, float inv, const LnParDot& p, XRow& xr) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const float4 r = *reinterpret_cast<const float4*>(row + (j * 64 + lane) * 4);
+        xr.x[j].x = ln_apply(r.x, mean, inv, p.g[j].x, p.b[j].x);
+        xr.x[j].y = ln_apply(r.y, mean, inv, p.g[j].y, p.b[j].y);
+        xr.x[j].z = ln_apply(r.z, mean, inv, p.g[j].z, p.b[j].z);
+        xr.x[j].w = ln_apply(r.w, mean, inv, p.g[j].w, p.b[j].w);
+    }
+}
+
 // One group of a wave's rows of a 1280-wide GEMV slice: rows k0 + 4 t (t = 0..3, those
 // below cnt), row k in ring chunk c0 + k.  The four dot products run interleaved and are
 // reduced together (wave_sum4): row k0 + 4 t ends in lanes 0-15, 32-47, 16-31, 48-63 for
-// t = 0, 1, 2, 3.  The group's chunks span 13 < kRing, so holding need at the first one while
-// waiting for the others cannot stall the loaders.
-__device__ __forceinline__ float rows4(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const float* xs, int wave, int lane,
+// t = 0, 1, 2, 3.  The group's chunks all come from one loader, which lands its chunks in
+// order, so one poll (for the last) covers them; they span 13 < kRing chunks, so holding
+// need at the first one cannot stall the loaders.
+__device__ __forceinline__ float rows4(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const XRow& xr, int wave, int lane,
                                        uint32_t* err, bool& failed) {
     release_to(ctl, c0 + k0, wave);
+    const int nt = min(4, (cnt - k0 + 3) >> 2);  // rows present, >= 1
+    (void)wait_chunk(ctl, ring, c0 + k0 + 4 * (nt - 1), err, failed);
     const float* ch[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int k = k0 + 4 * t;
-        ch[t] = k < cnt ? wait_chunk(ctl, ring, c0 + k, err, failed) : ch[0];  // absent rows re-read row k0
-    }
+    for (int t = 0; t < 4; ++t) ch[t] = ring + ((c0 + k0 + 4 * (t < nt ? t : 0)) % kRing) * kChunkF;  // absent rows re-read row k0
+    // all 20 reads first (the scheduler would otherwise issue each read right before its
+    // FMAs and wait for it, one LDS round trip per read)
+    float4 w[4][5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[t][j] = *reinterpret_cast<const float4*>(ch[t] + (j * 64 + lane) * 4);
+    __builtin_amdgcn_sched_barrier(0);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 5; ++j) {
-        const float4 x4 = *reinterpret_cast<const float4*>(xs + (j * 64 + lane) * 4);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const float4 w4 = *reinterpret_cast<const float4*>(ch[t] + (j * 64 + lane) * 4);
-            acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
-            acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
-            acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
-            acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
+            acc[t] = __builtin_fmaf(w[t][j].x, xr.x[j].x, acc[t]);
+            acc[t] = __builtin_fmaf(w[t][j].y, xr.x[j].y, acc[t]);
+            acc[t] = __builtin_fmaf(w[t][j].z, xr.x[j].z, acc[t]);
+            acc[t] = __builtin_fmaf(w[t][j].w, xr.x[j].w, acc[t]);
         }
     }
     return wave_sum4(acc[0], acc[1], acc[2], acc[3]);
 }
 
 // Runs a wave's rows k = wave + 4 i (< cnt) of a 1280-wide GEMV slice whose row k sits in
-// ring chunk c0 + k, four rows per reduction, and calls out(k, bias, sum) in the lane that
-// holds row k's sum.  Groups g < NG take their bias from `bias`, later ones from bias_mem.
+// ring chunk c0 + k, against the input x in registers, four rows per reduction, and calls
+// out(k, bias, sum) in the lane that holds row k's sum.  Groups g < NG take their bias from
+// `bias`, later ones from bias_mem.
 template <int NG, class Out>
-__device__ __forceinline__ void gemv_rows(Ctl& ctl, const float* ring, int c0, int cnt, const float* xs, const LaneBias<NG, false>& bias,
+__device__ __forceinline__ void gemv_rows(Ctl& ctl, const float* ring, int c0, int cnt, const XRow& xr, const LaneBias<NG, false>& bias,
                                           const float* __restrict__ bias_mem, int wave, int lane, uint32_t* err, bool& failed, Out out) {
     const int t = row_of_lane4(lane);
     const bool holder = (lane & 15) == 0;
@@ -495,13 +569,13 @@ __device__ __forceinline__ void gemv_rows(Ctl& ctl, const float* ring, int c0, i
     for (int g = 0; g < NG; ++g) {
         const int k0 = wave + 16 * g;
         if (k0 < cnt) {
-            const float v = rows4(ctl, ring, c0, k0, cnt, xs, wave, lane, err, failed);
+            const float v = rows4(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed);
             const int k = k0 + 4 * t;
             if (holder && k < cnt) out(k, bias.v[g], v);
         }
     }
     for (int k0 = wave + 16 * NG; k0 < cnt; k0 += 16) {
-        const float v = rows4(ctl, ring, c0, k0, cnt, xs, wave, lane, err, failed);
+        const float v = rows4(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed);
         const int k = k0 + 4 * t;
         if (holder && k < cnt) out(k, bias_mem[k], v);
     }
@@ -514,16 +588,24 @@ __device__ __forceinline__ float rows2_wide(Ctl& ctl, const float* ring, int c0,
                                             uint32_t* err, bool& failed) {
     const bool two = k0 + kCW < cnt;
     release_to(ctl, c0 + 4 * k0, wave);
+    // chunks c .. c + 3 of the later row come from the four loaders: one poll of all four
+    wait_run4(ctl, c0 + 4 * (two ? k0 + kCW : k0), err, failed);
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll 1
     for (int m = 0; m < 4; ++m) {
-        const float* c_0 = wait_chunk(ctl, ring, c0 + 4 * k0 + m, err, failed);
-        const float* c_1 = two ? wait_chunk(ctl, ring, c0 + 4 * (k0 + kCW) + m, err, failed) : c_0;
+        const float* c_0 = ring + ((c0 + 4 * k0 + m) % kRing) * kChunkF;
+        const float* c_1 = two ? ring + ((c0 + 4 * (k0 + kCW) + m) % kRing) * kChunkF : c_0;
+        float4 x4s[5], w0s[5], w1s[5];  // the 15 reads first, as in rows4
 #pragma unroll
         for (int j = 0; j < 5; ++j) {
-            const float4 x4 = *reinterpret_cast<const float4*>(xs + ((5 * m + j) * 64 + lane) * 4);
-            const float4 w0 = *reinterpret_cast<const float4*>(c_0 + (j * 64 + lane) * 4);
-            const float4 w1 = *reinterpret_cast<const float4*>(c_1 + (j * 64 + lane) * 4);
+            x4s[j] = *reinterpret_cast<const float4*>(xs + ((5 * m + j) * 64 + lane) * 4);
+            w0s[j] = *reinterpret_cast<const float4*>(c_0 + (j * 64 + lane) * 4);
+            w1s[j] = *reinterpret_cast<const float4*>(c_1 + (j * 64 + lane) * 4);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const float4 x4 = x4s[j], w0 = w0s[j], w1 = w1s[j];
             a0 = __builtin_fmaf(w0.x, x4.x, a0);
             a0 = __builtin_fmaf(w0.y, x4.y, a0);
             a0 = __builtin_fmaf(w0.z, x4.z, a0);
@@ -611,8 +693,8 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             }
             XRead<5> xr;
             xr.issue(X, idx, use, ep(l, kEpXh));
-            LnPar ln;
-            ln.load(par + kParLn1W, par + kParLn1B, tid);
+            LnParDot ln;
+            ln.load(par + kParLn1W, par + kParLn1B, lane);
             LaneBias<kGQkv, false> bias;
             bias.load(par + kParQkvB + P.q0, P.qn, wave, lane);
             float hv[5];
@@ -628,10 +710,14 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < 5; ++i) sm.hraw[tid + 256 * i] = hv[i];
-            ln256(hv, ln.g, ln.b, sm.red, tid, ctl, gen, a.err, failed);
-#pragma unroll
-            for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
             cbar(ctl, gen, a.err, failed);
+            XRow x;
+            {
+                float v[4][5], mean, inv;
+                ln_layout_load(sm.hraw, lane, v);
+                ln_stats(v, mean, inv);
+                ln_to_xrow(sm.hraw, lane, mean, inv, ln, x);
+            }
             const uint32_t e = ep(l, kEpQkv);
             auto out = [&](int k, float b, float acc) {  // called by the lane holding row k's sum
                 const int row = P.q0 + k;
@@ -644,7 +730,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                     a.kv[kvl + (is_v ? a.kv_v_off : 0) + (static_cast<size_t>(c >> 6) * a.kv_cap + n) * kHeadDim + (c & 63)] = v;
                 }
             };
-            gemv_rows(ctl, ring, cb, P.qn, sm.xs, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
+            gemv_rows(ctl, ring, cb, P.qn, x, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
         }
 
         // ------------------------------------------------ split-KV attention tiles
@@ -765,7 +851,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                         xst(part + 1, epart, ((sm.reds[0] + sm.reds[1]) + sm.reds[2]) + sm.reds[3]);
                     }
                 }
-                cbar(ctl, gen, a.err, failed);  // redm/reds/accs are reused by the next round
+                if (rd + 1 < P.rounds) cbar(ctl, gen, a.err, failed);  // redm/reds/accs are reused by the next round
             }
             release_to(ctl, cb + P.o_proj, wave);
         }
@@ -798,25 +884,31 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 }
             }
             cbar(ctl, gen, a.err, failed);
-            // wave w takes splits w, w+4, ... (attention_merge_kernel's order), straight from LDS
-            float m = -INFINITY;
-            for (int k = wave; k < P.S; k += 4) m = fmaxf(m, sm.mpart[k][0]);
-            if (lane == 0) sm.mwm[wave] = m;
-            cbar(ctl, gen, a.err, failed);
-            const float mg = fmaxf(fmaxf(sm.mwm[0], sm.mwm[1]), fmaxf(sm.mwm[2], sm.mwm[3]));
-            float den = 0.0f, num = 0.0f;
-            for (int k = wave; k < P.S; k += 4) {
-                const float mk = sm.mpart[k][0];
-                const float wgt = mk == -INFINITY ? 0.0f : expf(mk - mg);
-                den = __builtin_fmaf(sm.mpart[k][1], wgt, den);
-                num = __builtin_fmaf(sm.mpart[k][2 + lane], wgt, num);
-            }
-            sm.mwnum[wave][lane] = num;
-            if (lane == 0) sm.mwden[wave] = den;
-            cbar(ctl, gen, a.err, failed);
+            // Wave 0 merges, in attention_merge_kernel's order (decode.hip): its wave w takes
+            // splits w, w+4, ... and the four partial denominators and numerators are added in
+            // order.  Lane k computes split k's weight exp(m_k - max m) (S <= 64 splits); the
+            // sums then run over k with the weights broadcast from their lanes.  The maximum is
+            // exact in any order.
             if (wave == 0) {
-                const float d = ((sm.mwden[0] + sm.mwden[1]) + sm.mwden[2]) + sm.mwden[3];
-                const float nn = ((sm.mwnum[0][lane] + sm.mwnum[1][lane]) + sm.mwnum[2][lane]) + sm.mwnum[3][lane];
+                const int S = P.S;
+                const float mk = lane < S ? sm.mpart[lane][0] : -INFINITY;
+                const float lk = lane < S ? sm.mpart[lane][1] : 0.0f;
+                const float mg = wave_max(mk);
+                const float wk = mk == -INFINITY ? 0.0f : expf(mk - mg);
+                float den[4] = {0.0f, 0.0f, 0.0f, 0.0f}, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int k0 = 0; k0 < S; k0 += 4) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        const int k = k0 + w;
+                        if (k < S) {
+                            const float wgt = lane_value(wk, k);
+                            den[w] = __builtin_fmaf(lane_value(lk, k), wgt, den[w]);
+                            num[w] = __builtin_fmaf(sm.mpart[k][2 + lane], wgt, num[w]);
+                        }
+                    }
+                }
+                const float d = ((den[0] + den[1]) + den[2]) + den[3];
+                const float nn = ((num[0] + num[1]) + num[2]) + num[3];
                 xst(X + kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
             }
             cbar(ctl, gen, a.err, failed);  // mpart aliases xs, written below
@@ -844,12 +936,14 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = v[i];
             }
             cbar(ctl, gen, a.err, failed);
+            XRow x;
+            x.load(sm.xs, lane);
             const uint32_t e = ep(l, kEpHmid);
             auto out = [&](int k, float b, float acc) {
                 const int row = P.p0 + k;
                 xst(X + kXhmid + row, e, sm.hraw[row] + (acc + b));
             };
-            gemv_rows(ctl, ring, cp, P.pn, sm.xs, bias, par + kParProjB + P.p0, wave, lane, a.err, failed, out);
+            gemv_rows(ctl, ring, cp, P.pn, x, bias, par + kParProjB + P.p0, wave, lane, a.err, failed, out);
             release_to(ctl, cb + P.o_fc, wave);
         }
 
@@ -866,25 +960,28 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             }
             XRead<5> xr;
             xr.issue(X, idx, use, ep(l, kEpHmid));
-            LnPar ln;
-            ln.load(par + kParLn2W, par + kParLn2B, tid);
+            LnParDot ln;
+            ln.load(par + kParLn2W, par + kParLn2B, lane);
             LaneBias<kGFc, false> bias;
             bias.load(par + kParFcB + P.f0, P.fn, wave, lane);
             float hv[5];
             xr.wait(X, idx, ep(l, kEpHmid), hv, a.err, failed);
 #pragma unroll
             for (int i = 0; i < 5; ++i) sm.mraw[tid + 256 * i] = hv[i];
-            cbar(ctl, gen, a.err, failed);  // every wave is past its c_proj reads of xs
-            ln256(hv, ln.g, ln.b, sm.red, tid, ctl, gen, a.err, failed);
-#pragma unroll
-            for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
-            cbar(ctl, gen, a.err, failed);
+            cbar(ctl, gen, a.err, failed);  // also: every wave is past its c_proj reads of xs
+            XRow x;
+            {
+                float v[4][5], mean, inv;
+                ln_layout_load(sm.mraw, lane, v);
+                ln_stats(v, mean, inv);
+                ln_to_xrow(sm.mraw, lane, mean, inv, ln, x);
+            }
             const uint32_t e = ep(l, kEpFf);
             auto out = [&](int k, float b, float acc) {
                 const int row = P.f0 + k;
                 xst(X + kXff + row, e, gelu_f(acc + b));
             };
-            gemv_rows(ctl, ring, cf, P.fn, sm.xs, bias, par + kParFcB + P.f0, wave, lane, a.err, failed, out);
+            gemv_rows(ctl, ring, cf, P.fn, x, bias, par + kParFcB + P.f0, wave, lane, a.err, failed, out);
             release_to(ctl, cb + P.o_fc2, wave);
         }
 
@@ -904,7 +1001,8 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             xr.issue(X, idx, use, ep(l, kEpFf));
             LaneBias<kGFc2, true> bias;
             bias.load(par + kParFc2B + P.g0, P.gn, wave, lane);
-            cbar(ctl, gen, a.err, failed);  // every wave is past its c_fc reads of xs
+            // xs was last read by the c_proj phase, which every wave left before the c_fc
+            // phase's barrier
             {
                 float v[NF];
                 xr.wait(X, idx, ep(l, kEpFf), v, a.err, failed);
@@ -918,7 +1016,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             };
             gemv_rows_wide(ctl, ring, cg, P.gn, sm.xs, bias, par + kParFc2B + P.g0, wave, lane, a.err, failed, out);
             release_to(ctl, (l + 1) * P.layer_chunks, wave);
-            cbar(ctl, gen, a.err, failed);  // every wave is past its reads of xs and mraw
+            // xs and mraw are next written after the next layer's first barrier
         }
     }
 
@@ -935,20 +1033,36 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
         }
         XRead<5> xr;
         xr.issue(X, idx, use, ep(a.layers, kEpXh));
-        LnPar lf, fn;
+        LnPar lf;
         lf.load(a.head + kHeadLnfW, a.head + kHeadLnfB, tid);
-        fn.load(a.head + kHeadFnW, a.head + kHeadFnB, tid);
+        LnParDot fn;
+        fn.load(a.head + kHeadFnW, a.head + kHeadFnB, lane);
         LaneBias<kGHead, false> bias;
         bias.load(a.head + kHeadBias + P.h0, P.hn, wave, lane);
         float hv[5];
         xr.wait(X, idx, ep(a.layers, kEpXh), hv, a.err, failed);
-        ln256(hv, lf.g, lf.b, sm.red, tid, ctl, gen, a.err, failed);
-        ln256(hv, fn.g, fn.b, sm.red, tid, ctl, gen, a.err, failed);
+        // ln_f: statistics from the whole row, then this thread's five values to xs
 #pragma unroll
-        for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = hv[i];
+        for (int i = 0; i < 5; ++i) sm.hraw[tid + 256 * i] = hv[i];
         cbar(ctl, gen, a.err, failed);
+        {
+            float v[4][5], mean, inv;
+            ln_layout_load(sm.hraw, lane, v);
+            ln_stats(v, mean, inv);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = ln_apply(hv[i], mean, inv, lf.g[i], lf.b[i]);
+        }
+        cbar(ctl, gen, a.err, failed);
+        // final_norm of ln_f's output, straight into the GEMV's registers
+        XRow x;
+        {
+            float v[4][5], mean, inv;
+            ln_layout_load(sm.xs, lane, v);
+            ln_stats(v, mean, inv);
+            ln_to_xrow(sm.xs, lane, mean, inv, fn, x);
+        }
         auto out = [&](int k, float b, float acc) { a.logits[P.h0 + k] = acc + b; };
-        gemv_rows(ctl, ring, chd, P.hn, sm.xs, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
+        gemv_rows(ctl, ring, chd, P.hn, x, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
         release_to(ctl, total_chunks, wave);
     }
 }

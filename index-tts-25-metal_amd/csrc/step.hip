@@ -139,6 +139,12 @@ __device__ __forceinline__ int opaque_tid() {
 // i.e. for every load in flight (a loader's whole pipeline of staged loads, or a compute
 // wave's pending global stores).
 constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt/expcnt untouched
+constexpr int kWaitVm0 = 0x0F70;    // s_waitcnt vmcnt(0), lgkmcnt/expcnt untouched
+// End of a phase that published hand-off values: wait until this wave's stores are
+// acknowledged before it issues the next phase's polls and parameter loads.  Measured on
+// gfx950: letting the next phase's loads queue behind the stores in flight lengthens the
+// hand-off by more than the wait costs (0.8 vs 0.78 ms per step for the c_fc phase alone).
+__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(kWaitVm0); }
 __device__ __forceinline__ uint32_t lds_ld(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void lds_st(uint32_t* p, uint32_t v) {
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -406,7 +412,7 @@ __device__ __forceinline__ void run_loader(const StepArgs& a, const Plan& P, flo
             for (int k = 0; k < kLines; ++k) src[k] = W + lane * 4;
         }
 #pragma unroll
-        for (int k = 0; k < kLines; ++k) d[k] = *reinterpret_cast<const v4f*>(src[k]);
+        for (int k = 0; k < kLines; ++k) d[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(src[k]));
     };
 #pragma unroll
     for (int s = 0; s < kSlots; ++s) load(slot[s], s);
@@ -731,6 +737,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 }
             };
             gemv_rows(ctl, ring, cb, P.qn, x, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
+            stores_done();
         }
 
         // ------------------------------------------------ split-KV attention tiles
@@ -854,6 +861,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 if (rd + 1 < P.rounds) cbar(ctl, gen, a.err, failed);  // redm/reds/accs are reused by the next round
             }
             release_to(ctl, cb + P.o_proj, wave);
+            stores_done();
         }
 
         // ------------------------------------------------ merge of the splits of head h (workgroup h)
@@ -910,6 +918,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 const float d = ((den[0] + den[1]) + den[2]) + den[3];
                 const float nn = ((num[0] + num[1]) + num[2]) + num[3];
                 xst(X + kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
+                stores_done();
             }
             cbar(ctl, gen, a.err, failed);  // mpart aliases xs, written below
         }
@@ -945,6 +954,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             };
             gemv_rows(ctl, ring, cp, P.pn, x, bias, par + kParProjB + P.p0, wave, lane, a.err, failed, out);
             release_to(ctl, cb + P.o_fc, wave);
+            stores_done();
         }
 
         // ------------------------------------------------ LN2 + c_fc + GELU
@@ -983,6 +993,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             };
             gemv_rows(ctl, ring, cf, P.fn, x, bias, par + kParFcB + P.f0, wave, lane, a.err, failed, out);
             release_to(ctl, cb + P.o_fc2, wave);
+            stores_done();
         }
 
         // ------------------------------------------------ mlp.c_proj + residual -> next h
@@ -1016,6 +1027,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             };
             gemv_rows_wide(ctl, ring, cg, P.gn, sm.xs, bias, par + kParFc2B + P.g0, wave, lane, a.err, failed, out);
             release_to(ctl, (l + 1) * P.layer_chunks, wave);
+            stores_done();
             // xs and mraw are next written after the next layer's first barrier
         }
     }

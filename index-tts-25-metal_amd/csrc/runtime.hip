@@ -346,7 +346,7 @@ struct Engine {
         HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         HIP_CHECK(step_occupancy(false, &occ));
         if (occ < 1 || !step_fits(cus)) return;
-        xch.alloc(kStepExchange);
+        xch.alloc(kStepExchangeTotal);
         HIP_CHECK(hipMemsetAsync(xch.p, 0, xch.n * sizeof(uint64_t), stream));
         step_err.alloc(1);
         HIP_CHECK(hipMemsetAsync(step_err.p, 0, sizeof(uint32_t), stream));

@@ -74,6 +74,7 @@ constexpr int kXhmid = kXattn + kWidth;
 constexpr int kXff = kXhmid + kWidth;
 constexpr int kXpart = kXff + kFfn;
 static_assert(kXpart + kHeads * kAttnMaxSplits * 68 == kStepExchange, "exchange layout");
+static_assert(kXpart == kStepBroadcast, "broadcast vectors come first");
 
 enum Kind : uint32_t { kEpXh = 0, kEpQkv = 1, kEpPart = 2, kEpAttn = 3, kEpHmid = 4, kEpFf = 5 };
 
@@ -82,6 +83,15 @@ __device__ __forceinline__ uint64_t xld(const uint64_t* p) { return __hip_atomic
 __device__ __forceinline__ uint64_t xld(const uint64_t* base, int off) { return xld(base + static_cast<uint32_t>(off)); }
 __device__ __forceinline__ void xst(uint64_t* p, uint32_t epoch, float v) {
     __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Copy r of broadcast slot i (i < kStepBroadcast).
+__device__ __forceinline__ size_t xcopy(int r, int i) {
+    return r == 0 ? static_cast<size_t>(i) : size_t(kStepExchange) + size_t(r - 1) * kStepCopyStride + i;
+}
+// A broadcast value goes to every copy.
+__device__ __forceinline__ void xst_bcast(uint64_t* x, int i, uint32_t epoch, float v) {
+#pragma unroll
+    for (int r = 0; r < kStepCopies; ++r) xst(x + xcopy(r, i), epoch, v);
 }
 
 // N tagged values: issue() sends all loads, wait() retries the stale ones until their epoch
@@ -649,6 +659,8 @@ __device__ __forceinline__ void gemv_rows_wide(Ctl& ctl, const float* ring, int 
 // Row groups per compute wave whose biases are prefetched, per phase: all of them for the
 // slices of a 256-CU grid (15, 5, 20, 5 and 33 rows per workgroup).
 constexpr int kGQkv = 1, kGProj = 1, kGFc = 2, kGFc2 = 1, kGHead = 3;
+// Attention merges of at most this many splits run from registers (KV up to 1024 rows).
+constexpr int kMergeRegSplits = 16;
 
 __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
     __shared__ float ring[kRing * kChunkF];
@@ -675,7 +687,8 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
     // ================================================================ compute waves
     bool failed = false;
     uint32_t gen = 0;
-    uint64_t* __restrict__ X = a.xch;
+    uint64_t* __restrict__ X = a.xch;                             // copy 0: written by producers, partials
+    const uint64_t* __restrict__ XB = a.xch + xcopy(P.b % kStepCopies, 0);  // this workgroup's copy for reading
     const uint32_t e0 = a.epoch;
     auto ep = [&](int l, uint32_t kind) { return e0 + 8u * static_cast<uint32_t>(l) + kind; };
     const uint32_t n = P.n;
@@ -698,7 +711,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = l > 0;
             }
             XRead<5> xr;
-            xr.issue(X, idx, use, ep(l, kEpXh));
+            xr.issue(XB, idx, use, ep(l, kEpXh));
             LnParDot ln;
             ln.load(par + kParLn1W, par + kParLn1B, lane);
             LaneBias<kGQkv, false> bias;
@@ -712,7 +725,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                     hv[i] = a.mel_emb[static_cast<size_t>(st.token) * kWidth + c] + a.mel_pos[static_cast<size_t>(st.position) * kWidth + c];
                 }
             } else {
-                xr.wait(X, idx, ep(l, kEpXh), hv, a.err, failed);
+                xr.wait(XB, idx, ep(l, kEpXh), hv, a.err, failed);
             }
 #pragma unroll
             for (int i = 0; i < 5; ++i) sm.hraw[tid + 256 * i] = hv[i];
@@ -728,7 +741,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             auto out = [&](int k, float b, float acc) {  // called by the lane holding row k's sum
                 const int row = P.q0 + k;
                 const float v = acc + b;
-                xst(X + kXqkv + row, e, v);
+                xst_bcast(X, kXqkv + row, e, v);
                 if (row >= kWidth) {
                     const int rr = row - kWidth;
                     const bool is_v = rr >= kWidth;
@@ -778,7 +791,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                     use[4 + k] = use[8 + k] = i_new >= 0;
                 }
                 XRead<12> xr;
-                xr.issue(X, idx, use, eq);
+                xr.issue(XB, idx, use, eq);
                 // cached rows from the ring; need stays at the tile's first chunk until its rows
                 // are in registers
                 for (int j = 0; j < 2 * kc; ++j) (void)wait_chunk(ctl, ring, ca + j, a.err, failed);
@@ -798,7 +811,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 float4 q4;
                 {
                     float qv[12];
-                    xr.wait(X, idx, eq, qv, a.err, failed);
+                    xr.wait(XB, idx, eq, qv, a.err, failed);
                     q4 = make_float4(qv[0], qv[1], qv[2], qv[3]);
                     const float4 kn = make_float4(qv[4], qv[5], qv[6], qv[7]);
                     const float4 vn = make_float4(qv[8], qv[9], qv[10], qv[11]);
@@ -865,10 +878,51 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
         }
 
         // ------------------------------------------------ merge of the splits of head h (workgroup h)
-        if (P.b < kHeads) {
+        // In attention_merge_kernel's order (decode.hip): its wave w takes splits w, w+4, ...
+        // and the four partial denominators and numerators are added in order.  Lane k
+        // computes split k's weight exp(m_k - max m); the sums then run over k with the
+        // weights broadcast from their lanes.  The maximum is exact in any order.
+        if (P.b < kHeads && P.S <= kMergeRegSplits) {
+            // up to 16 splits: wave 0 reads the records straight into registers (lane d holds
+            // acc[k][d] for every k, lane k holds m_k and l_k) and merges them alone
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-            // The compute threads gather the S partial records (m, l, acc[64]) of head h into
-            // LDS, then merge them in the order of attention_merge_kernel (decode.hip).
+            if (wave == 0) {
+                const int h = P.b, S = P.S;
+                const uint64_t* pb = X + kXpart + static_cast<size_t>(h) * kAttnMaxSplits * 68;
+                constexpr int NR = kMergeRegSplits + 2;
+                int idx[NR];
+                bool use[NR];
+#pragma unroll
+                for (int k = 0; k < kMergeRegSplits; ++k) {
+                    idx[k] = k * 68 + 4 + lane;
+                    use[k] = k < S;
+                }
+                idx[kMergeRegSplits] = lane * 68;
+                idx[kMergeRegSplits + 1] = lane * 68 + 1;
+                use[kMergeRegSplits] = use[kMergeRegSplits + 1] = lane < S;
+                float v[NR];
+                xread<NR>(pb, idx, use, ep(l, kEpPart), v, a.err, failed);
+                const float mk = lane < S ? v[kMergeRegSplits] : -INFINITY;
+                const float lk = lane < S ? v[kMergeRegSplits + 1] : 0.0f;
+                const float mg = wave_max(mk);
+                const float wk = mk == -INFINITY ? 0.0f : expf(mk - mg);
+                float den[4] = {0.0f, 0.0f, 0.0f, 0.0f}, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < kMergeRegSplits; ++k) {
+                    if (k < S) {
+                        const float wgt = lane_value(wk, k);
+                        den[k & 3] = __builtin_fmaf(lane_value(lk, k), wgt, den[k & 3]);
+                        num[k & 3] = __builtin_fmaf(v[k], wgt, num[k & 3]);
+                    }
+                }
+                const float d = ((den[0] + den[1]) + den[2]) + den[3];
+                const float nn = ((num[0] + num[1]) + num[2]) + num[3];
+                xst_bcast(X, kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
+                stores_done();
+            }
+        } else if (P.b < kHeads) {
+            // more splits: the compute threads gather the records into LDS, wave 0 merges
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
             const int h = P.b;
             const uint64_t* pb = X + kXpart + static_cast<size_t>(h) * kAttnMaxSplits * 68;
             constexpr int kRec = 2 + kHeadDim;  // values used per record
@@ -892,11 +946,6 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 }
             }
             cbar(ctl, gen, a.err, failed);
-            // Wave 0 merges, in attention_merge_kernel's order (decode.hip): its wave w takes
-            // splits w, w+4, ... and the four partial denominators and numerators are added in
-            // order.  Lane k computes split k's weight exp(m_k - max m) (S <= 64 splits); the
-            // sums then run over k with the weights broadcast from their lanes.  The maximum is
-            // exact in any order.
             if (wave == 0) {
                 const int S = P.S;
                 const float mk = lane < S ? sm.mpart[lane][0] : -INFINITY;
@@ -917,7 +966,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 }
                 const float d = ((den[0] + den[1]) + den[2]) + den[3];
                 const float nn = ((num[0] + num[1]) + num[2]) + num[3];
-                xst(X + kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
+                xst_bcast(X, kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
                 stores_done();
             }
             cbar(ctl, gen, a.err, failed);  // mpart aliases xs, written below
@@ -935,12 +984,12 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = true;
             }
             XRead<5> xr;
-            xr.issue(X, idx, use, ep(l, kEpAttn));
+            xr.issue(XB, idx, use, ep(l, kEpAttn));
             LaneBias<kGProj, false> bias;
             bias.load(par + kParProjB + P.p0, P.pn, wave, lane);
             {
                 float v[5];
-                xr.wait(X, idx, ep(l, kEpAttn), v, a.err, failed);
+                xr.wait(XB, idx, ep(l, kEpAttn), v, a.err, failed);
 #pragma unroll
                 for (int i = 0; i < 5; ++i) sm.xs[tid + 256 * i] = v[i];
             }
@@ -950,7 +999,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             const uint32_t e = ep(l, kEpHmid);
             auto out = [&](int k, float b, float acc) {
                 const int row = P.p0 + k;
-                xst(X + kXhmid + row, e, sm.hraw[row] + (acc + b));
+                xst_bcast(X, kXhmid + row, e, sm.hraw[row] + (acc + b));
             };
             gemv_rows(ctl, ring, cp, P.pn, x, bias, par + kParProjB + P.p0, wave, lane, a.err, failed, out);
             release_to(ctl, cb + P.o_fc, wave);
@@ -969,13 +1018,13 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = true;
             }
             XRead<5> xr;
-            xr.issue(X, idx, use, ep(l, kEpHmid));
+            xr.issue(XB, idx, use, ep(l, kEpHmid));
             LnParDot ln;
             ln.load(par + kParLn2W, par + kParLn2B, lane);
             LaneBias<kGFc, false> bias;
             bias.load(par + kParFcB + P.f0, P.fn, wave, lane);
             float hv[5];
-            xr.wait(X, idx, ep(l, kEpHmid), hv, a.err, failed);
+            xr.wait(XB, idx, ep(l, kEpHmid), hv, a.err, failed);
 #pragma unroll
             for (int i = 0; i < 5; ++i) sm.mraw[tid + 256 * i] = hv[i];
             cbar(ctl, gen, a.err, failed);  // also: every wave is past its c_proj reads of xs
@@ -989,7 +1038,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             const uint32_t e = ep(l, kEpFf);
             auto out = [&](int k, float b, float acc) {
                 const int row = P.f0 + k;
-                xst(X + kXff + row, e, gelu_f(acc + b));
+                xst_bcast(X, kXff + row, e, gelu_f(acc + b));
             };
             gemv_rows(ctl, ring, cf, P.fn, x, bias, par + kParFcB + P.f0, wave, lane, a.err, failed, out);
             release_to(ctl, cb + P.o_fc2, wave);
@@ -1009,21 +1058,21 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = true;
             }
             XRead<NF> xr;
-            xr.issue(X, idx, use, ep(l, kEpFf));
+            xr.issue(XB, idx, use, ep(l, kEpFf));
             LaneBias<kGFc2, true> bias;
             bias.load(par + kParFc2B + P.g0, P.gn, wave, lane);
             // xs was last read by the c_proj phase, which every wave left before the c_fc
             // phase's barrier
             {
                 float v[NF];
-                xr.wait(X, idx, ep(l, kEpFf), v, a.err, failed);
+                xr.wait(XB, idx, ep(l, kEpFf), v, a.err, failed);
 #pragma unroll
                 for (int i = 0; i < NF; ++i) sm.xs[tid + kCT * i] = v[i];
             }
             cbar(ctl, gen, a.err, failed);
             auto out = [&](int k, float b, float acc) {
                 const int row = P.g0 + k;
-                xst(X + kXh + row, ep(l + 1, kEpXh), sm.mraw[row] + (acc + b));
+                xst_bcast(X, kXh + row, ep(l + 1, kEpXh), sm.mraw[row] + (acc + b));
             };
             gemv_rows_wide(ctl, ring, cg, P.gn, sm.xs, bias, par + kParFc2B + P.g0, wave, lane, a.err, failed, out);
             release_to(ctl, (l + 1) * P.layer_chunks, wave);
@@ -1044,7 +1093,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             use[i] = true;
         }
         XRead<5> xr;
-        xr.issue(X, idx, use, ep(a.layers, kEpXh));
+        xr.issue(XB, idx, use, ep(a.layers, kEpXh));
         LnPar lf;
         lf.load(a.head + kHeadLnfW, a.head + kHeadLnfB, tid);
         LnParDot fn;
@@ -1052,7 +1101,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
         LaneBias<kGHead, false> bias;
         bias.load(a.head + kHeadBias + P.h0, P.hn, wave, lane);
         float hv[5];
-        xr.wait(X, idx, ep(a.layers, kEpXh), hv, a.err, failed);
+        xr.wait(XB, idx, ep(a.layers, kEpXh), hv, a.err, failed);
         // ln_f: statistics from the whole row, then this thread's five values to xs
 #pragma unroll
         for (int i = 0; i < 5; ++i) sm.hraw[tid + 256 * i] = hv[i];

@@ -86,6 +86,39 @@ typedef struct itts_gpt_state itts_gpt_state;
  * weights transposed to [out, in] on the device), allocates the KV cache. */
 int itts_gpt_create(const itts_tensor* tensors, int32_t count, const itts_gpt_config* cfg, itts_gpt** out);
 void itts_gpt_destroy(itts_gpt* h);
+
+/* ---- MIT2 weight bundles (the reference's model format) ----------------------
+ * A directory (manifest.json + weights file) or a single file (weights stream +
+ * manifest + "MIT2VOIC" footer), memory-mapped.  itts_bundle_open performs the
+ * checks of mit2::Bundle::Bundle (vendor/metal-runtime/bundle.cpp:150-266) and of
+ * itts25::Weights::Weights (src/weights.cpp:9-28; require_model: the manifest names
+ * target "index-tts2.5"), with the same messages, reported by
+ * itts_bundle_last_error() (thread local; all are ITTS_ERUNTIME, as the reference's
+ * std::runtime_error).  Tensor data pointers stay valid until itts_bundle_close. */
+typedef struct itts_bundle itts_bundle;
+#define ITTS_DTYPE_F32 0u
+#define ITTS_DTYPE_U32 1u
+typedef struct {
+    const char* name;  /* owned by the bundle */
+    const void* data;  /* mapped bytes (host memory) */
+    int64_t shape[8];
+    int32_t ndim;
+    uint32_t dtype;    /* ITTS_DTYPE_F32 or ITTS_DTYPE_U32 */
+    uint64_t offset;   /* byte offset in the weights stream */
+    uint64_t nbytes;
+} itts_bundle_tensor;
+int itts_bundle_open(const char* path, int32_t require_model, itts_bundle** out);
+void itts_bundle_close(itts_bundle* b);
+const char* itts_bundle_last_error(void);
+int32_t itts_bundle_count(const itts_bundle* b);
+/* mit2::Bundle::tensors()[index] */
+int itts_bundle_tensor_at(const itts_bundle* b, int32_t index, itts_bundle_tensor* out);
+/* itts25::Weights::info (weights.cpp:29-33): "Missing tensor: <name>" when absent. */
+int itts_bundle_find(const itts_bundle* b, const char* name, itts_bundle_tensor* out);
+/* GptDecoder(Weights&, ...) (gpt.cpp:8-23) on a bundle: the GPT tensors by their
+ * reference names, uploaded straight from the mapping (f32 only, "Expected float32:
+ * <name>" otherwise).  Failures are reported by itts_gpt_last_error(NULL). */
+int itts_gpt_create_from_bundle(const itts_bundle* b, const itts_gpt_config* cfg, itts_gpt** out);
 const char* itts_gpt_last_error(const itts_gpt* h);
 
 /* GptDecoder::prepare (gpt.cpp:42-71): speaker[192], emotion[1280]; writes the

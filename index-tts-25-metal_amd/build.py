@@ -37,6 +37,8 @@ DEVICE_FLAGS = [
     f"-I{CSRC}",
 ]
 SOURCES = ["decode.hip", "step.hip", "sampler.hip", "beam.hip", "prefill.hip", "util.hip", "runtime.hip"]
+HOST_SOURCES = ["bundle.cpp"]  # host-only C++ (g++)
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -55,8 +57,15 @@ def build_library(jobs: int = 8) -> Path:
         _run([HIPCC, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
         return obj
 
-    with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(SOURCES)))) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+    def compile_host(src: str) -> Path:
+        obj = BUILD / (Path(src).stem + ".host.o")
+        _run(["g++", *HOST_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        return obj
+
+    with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(SOURCES) + len(HOST_SOURCES)))) as ex:
+        dev = ex.map(compile_one, SOURCES)
+        host = ex.map(compile_host, HOST_SOURCES)
+        objs = list(dev) + list(host)
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)

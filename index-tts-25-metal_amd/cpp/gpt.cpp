@@ -59,7 +59,7 @@ std::vector<float> apply_gpt_sampling_processors(const std::vector<float>& logit
     return out;
 }
 
-GptDecoder::GptDecoder(const std::vector<Tensor>& tensors, const itts_gpt_config* config) {
+itts_gpt* GptDecoder::create_from_tensors(const std::vector<Tensor>& tensors, const itts_gpt_config* config) {
     std::vector<itts_tensor> table;
     table.reserve(tensors.size());
     for (const auto& t : tensors) {
@@ -70,11 +70,76 @@ GptDecoder::GptDecoder(const std::vector<Tensor>& tensors, const itts_gpt_config
         for (size_t i = 0; i < t.shape.size() && i < 4; ++i) e.shape[i] = t.shape[i];
         table.push_back(e);
     }
-    const int st = itts_gpt_create(table.data(), static_cast<int32_t>(table.size()), config, &handle_);
+    itts_gpt* h = nullptr;
+    const int st = itts_gpt_create(table.data(), static_cast<int32_t>(table.size()), config, &h);
     if (st != ITTS_OK) rethrow(st, itts_gpt_last_error(nullptr));
+    return h;
 }
 
+itts_gpt* GptDecoder::create_from_bundle(const itts_bundle* bundle, const itts_gpt_config* config) {
+    itts_gpt* h = nullptr;
+    const int st = itts_gpt_create_from_bundle(bundle, config, &h);
+    if (st != ITTS_OK) rethrow(st, itts_gpt_last_error(nullptr));
+    return h;
+}
+
+itts_gpt* GptDecoder::create_from_path(const std::string& bundle_path, const itts_gpt_config* config) {
+    // the caller's Weights has already checked the model bundle (weights.cpp:10-28)
+    itts_bundle* b = nullptr;
+    if (itts_bundle_open(bundle_path.c_str(), 0, &b) != ITTS_OK) throw std::runtime_error(itts_bundle_last_error());
+    itts_gpt* h = nullptr;
+    const int st = itts_gpt_create_from_bundle(b, config, &h);
+    itts_bundle_close(b);  // the decoder holds device copies
+    if (st != ITTS_OK) rethrow(st, itts_gpt_last_error(nullptr));
+    return h;
+}
+
+GptDecoder::GptDecoder(const std::vector<Tensor>& tensors, const itts_gpt_config* config)
+    : handle_(create_from_tensors(tensors, config)) {}
+
+GptDecoder::GptDecoder(const itts_bundle* bundle, const itts_gpt_config* config) : handle_(create_from_bundle(bundle, config)) {}
+
 GptDecoder::~GptDecoder() { itts_gpt_destroy(handle_); }
+
+// ------------------------------------------------------------------ BundleWeights (weights.cpp:9-49)
+
+BundleWeights::BundleWeights(const std::string& path, bool require_model) {
+    if (itts_bundle_open(path.c_str(), require_model ? 1 : 0, &bundle_) != ITTS_OK) throw std::runtime_error(itts_bundle_last_error());
+}
+
+BundleWeights::~BundleWeights() { itts_bundle_close(bundle_); }
+
+const TensorInfo& BundleWeights::info(const std::string& name) const {
+    const auto found = infos_.find(name);
+    if (found != infos_.end()) return found->second;
+    itts_bundle_tensor t{};
+    if (itts_bundle_find(bundle_, name.c_str(), &t) != ITTS_OK) throw std::runtime_error(itts_bundle_last_error());
+    TensorInfo i;
+    i.name = t.name;
+    i.shape.assign(t.shape, t.shape + t.ndim);
+    i.dtype = t.dtype == ITTS_DTYPE_F32 ? "f32" : "u32";
+    i.offset = t.offset;
+    i.nbytes = t.nbytes;
+    return infos_.emplace(name, std::move(i)).first->second;
+}
+
+const std::vector<float>& BundleWeights::get(const std::string& name) {
+    const auto found = cache_.find(name);
+    if (found != cache_.end()) return found->second;
+    itts_bundle_tensor t{};
+    if (itts_bundle_find(bundle_, name.c_str(), &t) != ITTS_OK) throw std::runtime_error(itts_bundle_last_error());
+    if (t.dtype != ITTS_DTYPE_F32) throw std::runtime_error("Expected float32: " + name);
+    const float* p = static_cast<const float*>(t.data);
+    return cache_.emplace(name, std::vector<float>(p, p + t.nbytes / sizeof(float))).first->second;
+}
+
+std::vector<uint32_t> BundleWeights::ids(const std::string& name) const {
+    itts_bundle_tensor t{};
+    if (itts_bundle_find(bundle_, name.c_str(), &t) != ITTS_OK) throw std::runtime_error(itts_bundle_last_error());
+    if (t.dtype != ITTS_DTYPE_U32) throw std::runtime_error("Expected uint32: " + name);
+    const uint32_t* p = static_cast<const uint32_t*>(t.data);
+    return std::vector<uint32_t>(p, p + t.nbytes / sizeof(uint32_t));
+}
 
 void GptDecoder::check(int status) const {
     if (status != ITTS_OK) rethrow(status, itts_gpt_last_error(handle_));

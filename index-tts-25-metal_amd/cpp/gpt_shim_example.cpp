@@ -1,8 +1,8 @@
 // Example caller of the drop-in itts25::GptDecoder, written the way the reference's
 // pipeline holds it (src/pipeline.cpp:12, 23-25): a Weights object with info()/get(),
-// a device-context object, prepare -> generate.  Weights here are a synthetic 2-layer
-// table; `gpt_shim_example run` executes on the GPU, without arguments it only checks
-// that the shim links.
+// a device-context object, prepare -> generate.  `gpt_shim_example run` uses a synthetic
+// weight table; `gpt_shim_example bundle <dir>` loads a MIT2 bundle through itts25::BundleWeights;
+// both execute on the GPU.  Without arguments it only checks that the shim links.
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -33,7 +33,54 @@ struct TableWeights {  // the reference Weights interface (include/itts25/weight
 struct DeviceContext {};
 }  // namespace
 
+// `gpt_shim_example bundle <dir>`: the reference pipeline's construction
+// (src/pipeline.cpp:12; a Weights over the bundle, then GptDecoder gpt_(weights_, metal_)) on
+// a MIT2 bundle, then the same prepare -> greedy generate as `run`, printing the codes.
+// The shape of the reference's Weights as GptDecoder sees it: info/get plus bundle().root()
+// naming the MIT2 bundle (include/itts25/weights.hpp, include/mit2/bundle.hpp).  Its get()
+// is never called: the decoder re-opens bundle().root() and uploads from the mapping.
+struct RefStyleWeights {
+    struct Bundle {
+        std::string path;
+        const std::string& root() const { return path; }
+    } b;
+    itts25::BundleWeights inner;
+    explicit RefStyleWeights(const char* p) : b{p}, inner(p) {}
+    const Bundle& bundle() const { return b; }
+    const itts25::TensorInfo& info(const std::string& n) const { return inner.info(n); }
+    const std::vector<float>& get(const std::string&) { throw std::logic_error("get() should not be needed"); }
+};
+
+template <class W>
+int run_bundle_with(W& w) {
+    DeviceContext ctx;
+    itts25::GptDecoder gpt(w, ctx);
+    std::vector<float> speaker(192, 0.1f), emotion(1280, 0.05f);
+    auto prefix = gpt.prepare(speaker, emotion, {5, 17, 300, 1, 0, 42}, 3);
+    itts25::GenerationOptions opt;
+    opt.do_sample = false;
+    opt.repetition_penalty = 1;
+    auto r = gpt.generate(prefix, opt, 8);
+    std::printf("{\"rows\":%zu,\"codes\":[", prefix.size() / 1280);
+    for (size_t i = 0; i < r.codes.size(); ++i) std::printf("%s%u", i ? "," : "", r.codes[i]);
+    std::printf("],\"stopped\":%d,\"spk_shape\":[%lld,%lld]}\n", r.stopped ? 1 : 0,
+                static_cast<long long>(w.info("gpt.spk_emb_proj.weight").shape[0]),
+                static_cast<long long>(w.info("gpt.spk_emb_proj.weight").shape[1]));
+    return 0;
+}
+
+int run_bundle(const char* path, bool ref_style) {
+    if (ref_style) {
+        RefStyleWeights w(path);
+        return run_bundle_with(w);
+    }
+    itts25::BundleWeights w(path);
+    return run_bundle_with(w);
+}
+
 int main(int argc, char** argv) {
+    if (argc >= 3 && std::strcmp(argv[1], "bundle") == 0) return run_bundle(argv[2], false);
+    if (argc >= 3 && std::strcmp(argv[1], "refbundle") == 0) return run_bundle(argv[2], true);
     if (argc < 2 || std::strcmp(argv[1], "run") != 0) {
         std::printf("gpt shim linked\n");
         return 0;

@@ -9,9 +9,12 @@
 #include <cstdint>
 #include <memory>
 #include <string>
+#include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "itts_gpt.h"
+#include "itts25/bundle_weights.hpp"
 
 namespace itts25 {
 
@@ -49,10 +52,15 @@ public:
 
     // The reference accepts num_beams up to 10 on any decoder (gpt_sampling.cpp:172-173),
     // so the reference-form constructor provisions 10 KV slots (10 x 503 MB at capacity 4096).
-    template <class Weights, class Context>
-    GptDecoder(Weights& weights, Context& /*device context, unused*/) : GptDecoder(collect(weights), &kReferenceConfig) {}
+    // Weights types: the reference's Weights (its bundle().root() names the MIT2 bundle,
+    // which is re-opened here and uploaded straight from the mapping), this library's
+    // BundleWeights (the same, from its open bundle), or any type with info()/get() (the
+    // tensors are taken through get()).
+    template <class AnyWeights, class Context>
+    GptDecoder(AnyWeights& weights, Context& /*device context, unused*/) : handle_(create(weights)) {}
     static constexpr itts_gpt_config kReferenceConfig{4096, ITTS_MAX_BATCH, ITTS_WEIGHTS_F32, 0};
     explicit GptDecoder(const std::vector<Tensor>& tensors, const itts_gpt_config* config = nullptr);
+    GptDecoder(const itts_bundle* bundle, const itts_gpt_config* config);
     ~GptDecoder();
     GptDecoder(const GptDecoder&) = delete;
     GptDecoder& operator=(const GptDecoder&) = delete;
@@ -69,8 +77,26 @@ public:
 private:
     itts_gpt* handle_ = nullptr;
 
-    template <class Weights>
-    static std::vector<Tensor> collect(Weights& w) {
+    template <class W, class = void>
+    struct has_handle : std::false_type {};
+    template <class W>
+    struct has_handle<W, std::void_t<decltype(std::declval<const W&>().handle())>> : std::true_type {};
+    template <class W, class = void>
+    struct has_bundle_root : std::false_type {};
+    template <class W>
+    struct has_bundle_root<W, std::void_t<decltype(std::string(std::declval<W&>().bundle().root()))>> : std::true_type {};
+
+    static itts_gpt* create_from_bundle(const itts_bundle* bundle, const itts_gpt_config* config);
+    static itts_gpt* create_from_path(const std::string& bundle_path, const itts_gpt_config* config);
+    static itts_gpt* create_from_tensors(const std::vector<Tensor>& tensors, const itts_gpt_config* config);
+    template <class W>
+    static itts_gpt* create(W& w) {
+        if constexpr (has_handle<W>::value) return create_from_bundle(w.handle(), &kReferenceConfig);
+        else if constexpr (has_bundle_root<W>::value) return create_from_path(std::string(w.bundle().root()), &kReferenceConfig);
+        else return create_from_tensors(collect(w), &kReferenceConfig);
+    }
+    template <class AnyWeights>
+    static std::vector<Tensor> collect(AnyWeights& w) {
         std::vector<Tensor> out;
         auto add = [&](const std::string& name) { out.push_back({name, w.info(name).shape, &w.get(name)}); };
         for (const char* n : {"gpt.spk_emb_proj.weight", "gpt.spk_emb_proj.bias", "gpt.text_embedding.weight",

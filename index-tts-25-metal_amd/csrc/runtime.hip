@@ -1256,6 +1256,51 @@ int itts_gpt_create(const itts_tensor* tensors, int32_t count, const itts_gpt_co
     return ITTS_OK;
 }
 
+// GptDecoder(Weights&, ...) over a MIT2 bundle: the GPT tensors by the reference's names
+// (include/itts25/gpt.hpp collect list; gpt.cpp:8-23), zero-copy from the mapping.
+int itts_gpt_create_from_bundle(const itts_bundle* b, const itts_gpt_config* cfg, itts_gpt** out) {
+    if (!out) return ITTS_EINVAL;
+    *out = nullptr;
+    static const char* const kGlobal[] = {"gpt.spk_emb_proj.weight", "gpt.spk_emb_proj.bias", "gpt.text_embedding.weight",
+                                          "gpt.text_pos_embedding.emb.weight", "gpt.lang_embedding.weight",
+                                          "gpt.mel_embedding.weight", "gpt.mel_pos_embedding.emb.weight", "gpt.gpt.ln_f.weight",
+                                          "gpt.gpt.ln_f.bias", "gpt.final_norm.weight", "gpt.final_norm.bias",
+                                          "gpt.mel_head.weight", "gpt.mel_head.bias"};
+    static const char* const kLayer[] = {".ln_1.weight", ".ln_1.bias", ".attn.c_attn.weight", ".attn.c_attn.bias",
+                                         ".attn.c_proj.weight", ".attn.c_proj.bias", ".ln_2.weight", ".ln_2.bias",
+                                         ".mlp.c_fc.weight", ".mlp.c_fc.bias", ".mlp.c_proj.weight", ".mlp.c_proj.bias"};
+    std::vector<std::string> names;
+    std::vector<itts_tensor> list;
+    try {
+        if (!b) throw std::invalid_argument("Invalid bundle");
+        for (const char* n : kGlobal) names.emplace_back(n);
+        itts_bundle_tensor t{};
+        for (int i = 0;; ++i) {  // layers gpt.gpt.h.0 ... while the bundle has them (24 in IndexTTS 2.5)
+            const std::string p = "gpt.gpt.h." + std::to_string(i);
+            if (itts_bundle_find(b, (p + ".ln_1.weight").c_str(), &t) != ITTS_OK) break;
+            for (const char* s : kLayer) names.push_back(p + s);
+        }
+        for (const auto& n : names) {
+            if (itts_bundle_find(b, n.c_str(), &t) != ITTS_OK) throw std::runtime_error("Missing tensor: " + n);
+            if (t.dtype != ITTS_DTYPE_F32) throw std::runtime_error("Expected float32: " + n);
+            if (t.ndim > 4) throw std::invalid_argument("Invalid GPT tensor rank: " + n);
+            itts_tensor x{};
+            x.name = t.name;
+            x.data = static_cast<const float*>(t.data);
+            x.ndim = t.ndim;
+            for (int d = 0; d < t.ndim; ++d) x.shape[d] = t.shape[d];
+            list.push_back(x);
+        }
+    } catch (const std::invalid_argument& e) {
+        itts::g_create_error = e.what();
+        return ITTS_EINVAL;
+    } catch (const std::exception& e) {
+        itts::g_create_error = e.what();
+        return ITTS_ERUNTIME;
+    }
+    return itts_gpt_create(list.data(), static_cast<int32_t>(list.size()), cfg, out);
+}
+
 void itts_gpt_destroy(itts_gpt* h) { delete h; }
 
 const char* itts_gpt_last_error(const itts_gpt* h) { return h ? h->e.last_error.c_str() : itts::g_create_error.c_str(); }

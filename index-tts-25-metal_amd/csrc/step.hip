@@ -136,6 +136,12 @@ __device__ __forceinline__ void xread(const uint64_t* base, const int (&idx)[N],
     r.wait(base, idx, e, out, err, failed);
 }
 
+// A wave-uniform value through an empty asm: conditions derived from it are formed where
+// they are used instead of being hoisted out of the layer loop into spilled registers.
+__device__ __forceinline__ int opaque_s(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
 // threadIdx.x through an empty asm: per-thread offsets derived from it are recomputed in
 // each phase instead of being hoisted out of the layer loop and held live across phases.
 __device__ __forceinline__ int opaque_tid() {
@@ -887,7 +893,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             // acc[k][d] for every k, lane k holds m_k and l_k) and merges them alone
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
             if (wave == 0) {
-                const int h = P.b, S = P.S;
+                const int h = P.b, S = opaque_s(P.S);
                 const uint64_t* pb = X + kXpart + static_cast<size_t>(h) * kAttnMaxSplits * 68;
                 constexpr int NR = kMergeRegSplits + 2;
                 int idx[NR];

@@ -66,6 +66,11 @@ class _Options(C.Structure):
     ]
 
 
+class _BundleTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("data", C.c_void_p), ("shape", C.c_int64 * 8), ("ndim", C.c_int32), ("dtype", C.c_uint32),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64)]
+
+
 class _Timing(C.Structure):
     _fields_ = [("prefill_ms", C.c_float), ("decode_ms", C.c_float), ("decode_steps", C.c_uint32), ("decode_path", C.c_uint32)]
 
@@ -97,6 +102,13 @@ def _load() -> C.CDLL:
         "itts_gpt_last_timing": (C.c_int, [P, C.POINTER(_Timing)]),
         "itts_gpt_bench_kernel": (C.c_int, [P, i32, u32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
         "itts_synthetic_normal": (None, [f32p, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
+        "itts_bundle_open": (C.c_int, [C.c_char_p, i32, C.POINTER(P)]),
+        "itts_bundle_close": (None, [P]),
+        "itts_bundle_last_error": (C.c_char_p, []),
+        "itts_bundle_count": (i32, [P]),
+        "itts_bundle_tensor_at": (C.c_int, [P, i32, C.POINTER(_BundleTensor)]),
+        "itts_bundle_find": (C.c_int, [P, C.c_char_p, C.POINTER(_BundleTensor)]),
+        "itts_gpt_create_from_bundle": (C.c_int, [P, C.POINTER(_Config), C.POINTER(P)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -168,8 +180,143 @@ def _raise(status: int, msg: str) -> None:
     raise LogicError(msg)
 
 
+_DTYPES = {0: ("f32", np.float32), 1: ("u32", np.uint32)}
+
+
+class Bundle:
+    """A MIT2 weight bundle (directory or single file), memory-mapped: the reference's
+    mit2::Bundle (vendor/metal-runtime/bundle.cpp:150-293) with the checks of
+    itts25::Weights (src/weights.cpp:9-49).  get/ids/info mirror Weights."""
+
+    def __init__(self, path, require_model: bool = True):
+        self._b = C.c_void_p()
+        st = _lib.itts_bundle_open(str(path).encode(), 1 if require_model else 0, C.byref(self._b))
+        if st != 0:
+            _raise(st, _lib.itts_bundle_last_error().decode())
+        self.path = str(path)
+
+    def close(self) -> None:
+        if self._b.value:
+            _lib.itts_bundle_close(self._b)
+            self._b = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def __len__(self) -> int:
+        return int(_lib.itts_bundle_count(self._b))
+
+    @staticmethod
+    def _describe(t: "_BundleTensor") -> dict:
+        return {"name": t.name.decode(), "shape": tuple(int(t.shape[i]) for i in range(t.ndim)), "dtype": _DTYPES[t.dtype][0],
+                "offset": int(t.offset), "nbytes": int(t.nbytes)}
+
+    def tensors(self) -> List[dict]:
+        out = []
+        for i in range(len(self)):
+            t = _BundleTensor()
+            st = _lib.itts_bundle_tensor_at(self._b, i, C.byref(t))
+            if st != 0:
+                _raise(st, _lib.itts_bundle_last_error().decode())
+            out.append(self._describe(t))
+        return out
+
+    def _find(self, name: str) -> "_BundleTensor":
+        t = _BundleTensor()
+        st = _lib.itts_bundle_find(self._b, name.encode(), C.byref(t))
+        if st != 0:
+            _raise(st, _lib.itts_bundle_last_error().decode())
+        return t
+
+    def info(self, name: str) -> dict:
+        return self._describe(self._find(name))
+
+    def _array(self, name: str, want: int, what: str) -> np.ndarray:
+        t = self._find(name)
+        if t.dtype != want:
+            raise GptRuntimeError(f"Expected {what}: {name}")
+        dt = _DTYPES[t.dtype][1]
+        buf = (C.c_char * int(t.nbytes)).from_address(t.data)
+        a = np.frombuffer(buf, dtype=dt).copy()  # the mapping closes with the bundle
+        return a.reshape(tuple(int(t.shape[i]) for i in range(t.ndim)))
+
+    def get(self, name: str) -> np.ndarray:
+        """Weights::get (weights.cpp:34-42): a float32 tensor."""
+        return self._array(name, 0, "float32")
+
+    def ids(self, name: str) -> np.ndarray:
+        """Weights::ids (weights.cpp:43-48): a uint32 tensor."""
+        return self._array(name, 1, "uint32")
+
+
+def write_mit2_bundle(path, tensors: Dict[str, np.ndarray], single_file: bool = False, alignment: int = 4096,
+                      target: str = "index-tts2.5", weights_file: str = "weights.bin") -> Path:
+    """Writes tensors (float32 or uint32 arrays) as a MIT2 bundle: a directory with
+    manifest.json + weights_file, or one file with the manifest and the "MIT2VOIC" footer
+    appended.  Offsets are multiples of `alignment`; the stream starts with the 12-byte
+    header "MIT2", version 1, alignment."""
+    import hashlib
+    import json
+    import struct
+
+    path = Path(path)
+    records, blobs, pos = [], [], 12
+    for name, arr in tensors.items():
+        a = np.ascontiguousarray(arr)
+        if a.dtype == np.float32:
+            dtype = "f32"
+        elif a.dtype == np.uint32:
+            dtype = "u32"
+        else:
+            raise InvalidArgument(f"Unsupported bundle dtype {a.dtype}: {name}")
+        pos = (pos + alignment - 1) // alignment * alignment
+        data = a.tobytes()
+        records.append({"name": name, "shape": list(a.shape), "dtype": dtype, "offset": pos, "nbytes": len(data),
+                        "sha256": hashlib.sha256(data).hexdigest(), "layout": "row_major", "component": "gpt"})
+        blobs.append((pos, data))
+        pos += len(data)
+    manifest = {"format": "MIT2", "version": 1, "alignment": alignment, "endianness": "little", "weights_file": weights_file,
+                "metadata": {"target": target, "kind": "model"}, "tensors": records}
+    text = json.dumps(manifest).encode()
+
+    def write_stream(f) -> int:
+        f.write(b"MIT2" + struct.pack("<II", 1, alignment))
+        for off, data in blobs:
+            f.seek(off)
+            f.write(data)
+        return max([12] + [off + len(d) for off, d in blobs])
+
+    if single_file:
+        with open(path, "wb") as f:
+            end = write_stream(f)
+            f.seek(end)
+            f.write(text)
+            f.write(struct.pack("<QQ", end, len(text)) + b"MIT2VOIC")
+    else:
+        path.mkdir(parents=True, exist_ok=True)
+        with open(path / weights_file, "wb") as f:
+            write_stream(f)
+        (path / "manifest.json").write_bytes(text)
+    return path
+
+
 class GptDecoder:
     """itts25::GptDecoder on one MI355X (gpt.hpp:22-43)."""
+
+    @classmethod
+    def from_bundle(cls, bundle: "Bundle", kv_capacity: int = 4096, max_batch: int = 1, weight_dtype: str = "f32") -> "GptDecoder":
+        """GptDecoder(Weights&, ...) on a MIT2 bundle: the GPT tensors go to the device
+        straight from the bundle's mapping."""
+        self = cls.__new__(cls)
+        self._h = C.c_void_p()
+        self._keep = []
+        cfg = _Config(int(kv_capacity), int(max_batch), 1 if weight_dtype == "bf16" else 0, 0)
+        st = _lib.itts_gpt_create_from_bundle(bundle._b, C.byref(cfg), C.byref(self._h))
+        if st != 0:
+            _raise(st, _lib.itts_gpt_last_error(None).decode())
+        self.kv_capacity = int(kv_capacity)
+        self.max_batch = int(max_batch)
+        return self
 
     def __init__(self, weights: Optional[Dict[str, np.ndarray]], kv_capacity: int = 4096, max_batch: int = 1,
                  weight_dtype: str = "f32"):

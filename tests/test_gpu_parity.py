@@ -333,3 +333,25 @@ def test_persistent_generate_equals_multikernel(both_paths, itts):
     b = multi.generate(prefix, o, 96)
     assert (a.codes, a.stopped) == (b.codes, b.stopped)
     assert step.cached_tokens() == multi.cached_tokens()
+
+
+@pytest.mark.gpu
+def test_decoder_from_bundle_bitwise_equals_arrays(itts, small_weights, tmp_path):
+    """GptDecoder.from_bundle (zero-copy from the mapping) and GptDecoder(arrays) upload the
+    same weights: identical prefill logits, steps and sampled codes."""
+    for single in (False, True):
+        path = itts.write_mit2_bundle(tmp_path / ("one.mit2" if single else "dir"), small_weights, single_file=single)
+        b = itts.Bundle(path, require_model=not single)
+        a = itts.GptDecoder(small_weights, kv_capacity=1024)
+        d = itts.GptDecoder.from_bundle(b, kv_capacity=1024)
+        b.close()  # the decoder holds device copies; the mapping is no longer needed
+        cond, ids = itts.synthetic_prefix_inputs(40, seed=5)
+        prefix = a.prepare_cond(cond, ids, 3)
+        la, ld = a.prefill(prefix), d.prefill(prefix)
+        assert np.array_equal(la, ld)
+        assert np.array_equal(a.step(17, 2), d.step(17, 2))
+        opt = itts.GenerationOptions(seed=9, temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=10.0)
+        ra, rd = a.generate(prefix, opt, 24), d.generate(prefix, opt, 24)
+        assert list(ra.codes) == list(rd.codes) and ra.stopped == rd.stopped
+        a.close()
+        d.close()

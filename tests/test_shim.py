@@ -4,6 +4,7 @@ import json
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 EXE = Path(__file__).resolve().parent.parent / "index-tts-25-metal_amd" / "cpp" / "gpt_shim_example"
@@ -26,3 +27,26 @@ def test_shim_runs_on_gpu():
     assert lines[0]["codes"] + lines[0]["stopped"] >= 1
     assert lines[1]["beam_codes"] + lines[1]["beam_stopped"] >= 1
     assert lines[2]["processed"] == 8194
+
+
+@pytest.mark.gpu
+def test_shim_bundle_matches_python_decoder(itts, small_weights, tmp_path):
+    """Weights(path) + GptDecoder(weights, ctx) on a MIT2 bundle of the 2-layer model gives
+    the codes the Python decoder gives from the same arrays."""
+    assert EXE.exists(), "shim example not built"
+    bundle = itts.write_mit2_bundle(tmp_path / "gpt2l", small_weights)
+    outs = []
+    for mode in ("bundle", "refbundle"):  # BundleWeights, and a reference-style Weights (bundle().root())
+        out = subprocess.run([str(EXE), mode, str(bundle)], capture_output=True, text=True, timeout=300)
+        assert out.returncode == 0, out.stdout + out.stderr
+        outs.append([json.loads(l) for l in out.stdout.splitlines() if l.startswith("{")][0])
+    got = outs[0]
+    assert outs[1] == got
+    dec = itts.GptDecoder(small_weights, kv_capacity=4096)
+    prefix = dec.prepare(np.full(192, 0.1, np.float32), np.full(1280, 0.05, np.float32), [5, 17, 300, 1, 0, 42], 3)
+    opt = itts.GenerationOptions(do_sample=False, repetition_penalty=1.0)
+    r = dec.generate(prefix, opt, 8)
+    dec.close()
+    assert got["rows"] == prefix.size // 1280
+    assert got["codes"] == list(r.codes) and bool(got["stopped"]) == bool(r.stopped)
+    assert got["spk_shape"] == [1280, 192]

@@ -548,33 +548,41 @@ __device__ __forceinline__ void ln_to_xrow(const float* row, int lane, float mea
 // t = 0, 1, 2, 3.  The group's chunks all come from one loader, which lands its chunks in
 // order, so one poll (for the last) covers them; they span 13 < kRing chunks, so holding
 // need at the first one cannot stall the loaders.
-__device__ __forceinline__ float rows4(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const XRow& xr, int wave, int lane,
-                                       uint32_t* err, bool& failed) {
+// N = 5: the same with a fifth row k0 + 16 (its chunks span 17 < kRing), reduced alone
+// (wave_sum, every lane) into *fifth: a wave's last five rows in one pass instead of a
+// group of four followed by a group of one.
+template <int N>
+__device__ __forceinline__ float rowsN(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const XRow& xr, int wave, int lane,
+                                       uint32_t* err, bool& failed, float* fifth) {
+    static_assert(N == 4 || N == 5, "row group size");
     release_to(ctl, c0 + k0, wave);
-    const int nt = min(4, (cnt - k0 + 3) >> 2);  // rows present, >= 1
+    const int nt = N == 5 ? 5 : min(4, (cnt - k0 + 3) >> 2);  // rows present, >= 1
     (void)wait_chunk(ctl, ring, c0 + k0 + 4 * (nt - 1), err, failed);
-    const float* ch[4];
+    const float* ch[N];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) ch[t] = ring + ((c0 + k0 + 4 * (t < nt ? t : 0)) % kRing) * kChunkF;  // absent rows re-read row k0
-    // all 20 reads first (the scheduler would otherwise issue each read right before its
+    for (int t = 0; t < N; ++t) ch[t] = ring + ((c0 + k0 + 4 * (t < nt ? t : 0)) % kRing) * kChunkF;  // absent rows re-read row k0
+    // all reads first (the scheduler would otherwise issue each read right before its
     // FMAs and wait for it, one LDS round trip per read)
-    float4 w[4][5];
+    float4 w[N][5];
 #pragma unroll
     for (int j = 0; j < 5; ++j)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) w[t][j] = *reinterpret_cast<const float4*>(ch[t] + (j * 64 + lane) * 4);
+        for (int t = 0; t < N; ++t) w[t][j] = *reinterpret_cast<const float4*>(ch[t] + (j * 64 + lane) * 4);
     __builtin_amdgcn_sched_barrier(0);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[N];
+#pragma unroll
+    for (int t = 0; t < N; ++t) acc[t] = 0.0f;
 #pragma unroll
     for (int j = 0; j < 5; ++j) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < N; ++t) {
             acc[t] = __builtin_fmaf(w[t][j].x, xr.x[j].x, acc[t]);
             acc[t] = __builtin_fmaf(w[t][j].y, xr.x[j].y, acc[t]);
             acc[t] = __builtin_fmaf(w[t][j].z, xr.x[j].z, acc[t]);
             acc[t] = __builtin_fmaf(w[t][j].w, xr.x[j].w, acc[t]);
         }
     }
+    if constexpr (N == 5) *fifth = wave_sum(acc[4]);
     return wave_sum4(acc[0], acc[1], acc[2], acc[3]);
 }
 
@@ -587,19 +595,60 @@ __device__ __forceinline__ void gemv_rows(Ctl& ctl, const float* ring, int c0, i
                                           const float* __restrict__ bias_mem, int wave, int lane, uint32_t* err, bool& failed, Out out) {
     const int t = row_of_lane4(lane);
     const bool holder = (lane & 15) == 0;
+    bool done = false;  // the previous group took this one's row as its fifth
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
         const int k0 = wave + 16 * g;
-        if (k0 < cnt) {
-            const float v = rows4(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed);
+        if (k0 < cnt && !done) {
             const int k = k0 + 4 * t;
-            if (holder && k < cnt) out(k, bias.v[g], v);
+            if (k0 + 16 < cnt && k0 + 20 >= cnt) {  // exactly five rows left
+                float v5;
+                const float v = rowsN<5>(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed, &v5);
+                if (holder && k < cnt) out(k, bias.v[g], v);
+                if (lane == 0) out(k0 + 16, g + 1 < NG ? bias.v[g + 1 < NG ? g + 1 : 0] : bias_mem[k0 + 16], v5);
+                done = true;
+            } else {
+                const float v = rowsN<4>(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed, nullptr);
+                if (holder && k < cnt) out(k, bias.v[g], v);
+            }
         }
     }
+    if (done) return;
     for (int k0 = wave + 16 * NG; k0 < cnt; k0 += 16) {
-        const float v = rows4(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed);
         const int k = k0 + 4 * t;
+        if (k0 + 16 < cnt && k0 + 20 >= cnt) {
+            float v5;
+            const float v = rowsN<5>(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed, &v5);
+            if (holder && k < cnt) out(k, bias_mem[k], v);
+            if (lane == 0) out(k0 + 16, bias_mem[k0 + 16], v5);
+            return;
+        }
+        const float v = rowsN<4>(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed, nullptr);
         if (holder && k < cnt) out(k, bias_mem[k], v);
+    }
+}
+
+// Chunk m (1280 columns) of two 5120-wide rows: the input's 5 float4 and the rows' 10.
+__device__ __forceinline__ void wide_load(const float* xs, const float* c0, const float* c1, int m, int lane, float4 (&x)[5],
+                                          float4 (&w0)[5], float4 (&w1)[5]) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        x[j] = *reinterpret_cast<const float4*>(xs + ((5 * m + j) * 64 + lane) * 4);
+        w0[j] = *reinterpret_cast<const float4*>(c0 + (j * 64 + lane) * 4);
+        w1[j] = *reinterpret_cast<const float4*>(c1 + (j * 64 + lane) * 4);
+    }
+}
+__device__ __forceinline__ void wide_fma(const float4 (&x)[5], const float4 (&w0)[5], const float4 (&w1)[5], float& a0, float& a1) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        a0 = __builtin_fmaf(w0[j].x, x[j].x, a0);
+        a0 = __builtin_fmaf(w0[j].y, x[j].y, a0);
+        a0 = __builtin_fmaf(w0[j].z, x[j].z, a0);
+        a0 = __builtin_fmaf(w0[j].w, x[j].w, a0);
+        a1 = __builtin_fmaf(w1[j].x, x[j].x, a1);
+        a1 = __builtin_fmaf(w1[j].y, x[j].y, a1);
+        a1 = __builtin_fmaf(w1[j].z, x[j].z, a1);
+        a1 = __builtin_fmaf(w1[j].w, x[j].w, a1);
     }
 }
 
@@ -612,32 +661,31 @@ __device__ __forceinline__ float rows2_wide(Ctl& ctl, const float* ring, int c0,
     release_to(ctl, c0 + 4 * k0, wave);
     // chunks c .. c + 3 of the later row come from the four loaders: one poll of all four
     wait_run4(ctl, c0 + 4 * (two ? k0 + kCW : k0), err, failed);
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 1
+    // the four 1280-column chunks in a two-stage pipeline: chunk m + 1's 15 LDS reads are in
+    // flight while chunk m's FMAs run
+    const float* c_0[4];
+    const float* c_1[4];
+#pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const float* c_0 = ring + ((c0 + 4 * k0 + m) % kRing) * kChunkF;
-        const float* c_1 = two ? ring + ((c0 + 4 * (k0 + kCW) + m) % kRing) * kChunkF : c_0;
-        float4 x4s[5], w0s[5], w1s[5];  // the 15 reads first, as in rows4
-#pragma unroll
-        for (int j = 0; j < 5; ++j) {
-            x4s[j] = *reinterpret_cast<const float4*>(xs + ((5 * m + j) * 64 + lane) * 4);
-            w0s[j] = *reinterpret_cast<const float4*>(c_0 + (j * 64 + lane) * 4);
-            w1s[j] = *reinterpret_cast<const float4*>(c_1 + (j * 64 + lane) * 4);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < 5; ++j) {
-            const float4 x4 = x4s[j], w0 = w0s[j], w1 = w1s[j];
-            a0 = __builtin_fmaf(w0.x, x4.x, a0);
-            a0 = __builtin_fmaf(w0.y, x4.y, a0);
-            a0 = __builtin_fmaf(w0.z, x4.z, a0);
-            a0 = __builtin_fmaf(w0.w, x4.w, a0);
-            a1 = __builtin_fmaf(w1.x, x4.x, a1);
-            a1 = __builtin_fmaf(w1.y, x4.y, a1);
-            a1 = __builtin_fmaf(w1.z, x4.z, a1);
-            a1 = __builtin_fmaf(w1.w, x4.w, a1);
-        }
+        c_0[m] = ring + ((c0 + 4 * k0 + m) % kRing) * kChunkF;
+        c_1[m] = two ? ring + ((c0 + 4 * (k0 + kCW) + m) % kRing) * kChunkF : c_0[m];
     }
+    float4 xa[5], wa0[5], wa1[5], xb[5], wb0[5], wb1[5];
+    float a0 = 0.0f, a1 = 0.0f;
+    wide_load(xs, c_0[0], c_1[0], 0, lane, xa, wa0, wa1);
+    wide_load(xs, c_0[1], c_1[1], 1, lane, xb, wb0, wb1);
+    __builtin_amdgcn_sched_barrier(0);
+    wide_fma(xa, wa0, wa1, a0, a1);
+    __builtin_amdgcn_sched_barrier(0);
+    wide_load(xs, c_0[2], c_1[2], 2, lane, xa, wa0, wa1);
+    __builtin_amdgcn_sched_barrier(0);
+    wide_fma(xb, wb0, wb1, a0, a1);
+    __builtin_amdgcn_sched_barrier(0);
+    wide_load(xs, c_0[3], c_1[3], 3, lane, xb, wb0, wb1);
+    __builtin_amdgcn_sched_barrier(0);
+    wide_fma(xa, wa0, wa1, a0, a1);
+    __builtin_amdgcn_sched_barrier(0);
+    wide_fma(xb, wb0, wb1, a0, a1);
     return wave_sum2(a0, a1);
 }
 template <int NG, class Out>

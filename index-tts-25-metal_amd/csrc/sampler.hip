@@ -15,10 +15,19 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SampleArgs a) {
     const bool processors = a.mode != kModeDraw;
     const bool need_sample = a.mode == kModeDraw || (a.mode == kModeDecode && st.do_sample);
     const float* lg = a.logits + static_cast<size_t>(b) * a.logit_stride;
-    for (int i = t; i < V; i += NT) {
-        float v = lg[i];
-        if (processors && st.suppress_stop && (i == kMelStart || i == kMelStop)) v = -INFINITY;
-        sm.s[i] = v;
+    {
+        float v[IPT];  // all loads in flight before the first store
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            v[q] = i < V ? lg[i] : 0.0f;
+        }
+        const bool drop_stop = processors && st.suppress_stop;
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V) sm.s[i] = drop_stop && (i == kMelStart || i == kMelStop) ? -INFINITY : v[q];
+        }
     }
     __syncthreads();
     double* Pg = a.probs + static_cast<size_t>(b) * V;
@@ -46,15 +55,16 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SampleArgs a) {
                     __syncthreads();
                 }
             }
-            if (status == kOk && t == 0) {
+            if (status == kOk && t < 64) {
+                // wave 0 draws; every lane holds the same rng, token and status
                 const double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : Pg;
                 uint64_t rng = st.rng;
                 const int draws = a.mode == kModeDraw ? a.draws : 1;
                 for (int d = 0; d < draws && status == kOk; ++d) {
-                    token = draw_token(sm, m, P, rng, &status);
-                    if (a.mode == kModeDraw) a.out_tokens[d] = token;
+                    token = draw_token_wave(sm, m, P, rng, &status);
+                    if (a.mode == kModeDraw && t == 0) a.out_tokens[d] = token;
                 }
-                st.rng = rng;
+                if (t == 0) st.rng = rng;
             }
         }
     }

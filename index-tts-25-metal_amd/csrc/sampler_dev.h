@@ -12,9 +12,11 @@
 //                            target = u * total, first i with target < cumulative,
 //                            else the last positive one;
 //   splitmix_*      :11-26   SplitMix64.
-// Only ordering-free work runs in parallel (elementwise ops, a radix select for the
-// top-k pivot, index-order compaction, a bitonic sort of survivors).  Every floating-
-// point sum the reference forms sequentially is formed by one thread in the same order.
+// Only ordering-free work runs in parallel (elementwise ops, a radix select for the top-k
+// pivot, index-order compaction, a bitonic sort of survivors, the divisions of top-p).  Every floating-point
+// sum the reference forms sequentially is formed by one lane in the same order: wave 0
+// loads 64 terms at a time into its lanes and lane-serial code reads them back with
+// v_readlane, so the chain of adds waits on no LDS round trip.
 #pragma once
 #include "kernels.h"
 
@@ -24,7 +26,7 @@ namespace sampling {
 constexpr int V = kMelVocab;
 constexpr int NT = 1024;
 constexpr int NWAVE = NT / 64;
-constexpr int IPT = (V + NT - 1) / NT;  // contiguous indices per thread for compaction (9)
+constexpr int IPT = (V + NT - 1) / NT;  // score entries per thread (9): i = t + q * NT, q < IPT
 constexpr int kSortMax = 16384;          // next power of two >= V
 constexpr int kSmallProbs = 1024;
 constexpr uint16_t kRemoved = 0x8000;
@@ -43,6 +45,7 @@ struct Smem {
         uint64_t sortbuf[kSortMax];
     };
     uint16_t list[V];  // finite survivors in index order; bit 15 = removed by top-p
+    uint32_t qoff[IPT][NWAVE];  // compaction: survivors before (q, wave) in index order
     double probs[kSmallProbs];
     uint32_t hist[256];
     uint32_t wtot[NWAVE];
@@ -67,6 +70,17 @@ __device__ __forceinline__ double splitmix_unit(uint64_t& state) {
 
 __device__ __forceinline__ bool finite_f(float v) { return fabsf(v) <= 3.402823466e38f; }
 
+// Lane l's value of a wave-uniform lane index l (v_readlane; the halves are widened as
+// unsigned so no sign bit leaks into the other half).
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+    const uint64_t lo = readlane_u32(static_cast<uint32_t>(u), l);
+    const uint64_t hi = readlane_u32(static_cast<uint32_t>(u >> 32), l);
+    return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
 // kk-th largest value (1-based) of s[0..V): MSB-first radix select on order-preserving keys.
 __device__ inline float radix_kth_largest(Smem& sm, uint32_t kk) {
     const int t = threadIdx.x, lane = t & 63;
@@ -119,45 +133,62 @@ __device__ inline float radix_kth_largest(Smem& sm, uint32_t kk) {
     return key_float(prefix);
 }
 
-// Compact finite entries of s into sm.list (index order); returns the count, sets sm.mx.
+// Compact finite entries of s into sm.list (index order); returns the count, sets sm.m and
+// sm.mx.  Entry i = t + q * NT sits at position (q, t) in index order, so a ballot per
+// (q, wave) plus one exclusive scan over the IPT x NWAVE counts places every survivor.
 __device__ inline uint32_t compact_finite(Smem& sm) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int i0 = t * IPT, i1 = min(V, i0 + IPT);
-    uint32_t c = 0;
+    uint64_t bal[IPT];
     float mloc = -INFINITY;
-    for (int i = i0; i < i1; ++i) {
-        const float v = sm.s[i];
-        if (finite_f(v)) {
-            ++c;
-            mloc = fmaxf(mloc, v);
-        }
-    }
-    uint32_t inc = c;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += v;
+    for (int q = 0; q < IPT; ++q) {
+        const int i = t + q * NT;
+        const float v = i < V ? sm.s[i] : -INFINITY;
+        const bool f = i < V && finite_f(v);
+        if (f) mloc = fmaxf(mloc, v);
+        bal[q] = __ballot(f);
     }
     const float wm = wave_max(mloc);
-    if (lane == 63) sm.wtot[wave] = inc;
-    if (lane == 0) sm.wmax[wave] = wm;
-    __syncthreads();
-    uint32_t off = 0, total = 0;
-    float mx = -INFINITY;
-    for (int w = 0; w < NWAVE; ++w) {
-        if (w < wave) off += sm.wtot[w];
-        total += sm.wtot[w];
-        mx = fmaxf(mx, sm.wmax[w]);
-    }
-    off += inc - c;
-    for (int i = i0; i < i1; ++i)
-        if (finite_f(sm.s[i])) sm.list[off++] = static_cast<uint16_t>(i);
-    if (t == 0) {
-        sm.m = total;
-        sm.mx = mx;
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) sm.qoff[q][wave] = static_cast<uint32_t>(__popcll(bal[q]));
+        sm.wmax[wave] = wm;
     }
     __syncthreads();
-    return total;
+    if (wave == 0) {
+        // exclusive scan of the counts in (q, wave) order, 64 at a time
+        constexpr int kCells = IPT * NWAVE;
+        uint32_t* cell = &sm.qoff[0][0];
+        uint32_t carry = 0;
+        for (int c0 = 0; c0 < kCells; c0 += 64) {
+            const int f = c0 + lane;
+            const uint32_t cnt = f < kCells ? cell[f] : 0u;
+            uint32_t inc = cnt;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += v;
+            }
+            if (f < kCells) cell[f] = carry + inc - cnt;
+            carry += readlane_u32(inc, 63);
+        }
+        const float mx = wave_max(lane < NWAVE ? sm.wmax[lane] : -INFINITY);
+        if (lane == 0) {
+            sm.m = carry;
+            sm.mx = mx;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+        if ((bal[q] >> lane) & 1ull) {
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[q] >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[q]), 0u));
+            sm.list[sm.qoff[q][wave] + below] = static_cast<uint16_t>(t + q * NT);
+        }
+    }
+    __syncthreads();
+    return sm.m;
 }
 
 // First index of the maximum (std::max_element semantics).
@@ -243,11 +274,21 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
     const int t = threadIdx.x;
     *topp_ran = false;
     if (pen != 1.0f || T != 1.0f) {
-        for (int i = t; i < V; i += NT) {
-            float v = sm.s[i];
-            if (pen != 1.0f && seen[i]) v = v < 0.0f ? v * pen : v / pen;
-            if (T != 1.0f) v = v / T;
-            sm.s[i] = v;
+        uint8_t hit[IPT];
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            hit[q] = pen != 1.0f && i < V ? seen[i] : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V) {
+                float v = sm.s[i];
+                if (hit[q]) v = v < 0.0f ? v * pen : v / pen;
+                if (T != 1.0f) v = v / T;
+                sm.s[i] = v;
+            }
         }
         __syncthreads();
     }
@@ -282,22 +323,39 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
     }
     __syncthreads();
     bitonic_sort(sm, n);
-    if (t == 0) {
+    if (t < 64) {
+        // total in index order, then the cumulative mass in ascending (score, index) order:
+        // the divisions P[j] / total run in parallel, the two sums lane-serially.
+        const int lane = t;
         double total = 0.0;
-        for (uint32_t j = 0; j < m; ++j) total += P[j];
+        for (uint32_t c0 = 0; c0 < m; c0 += 64) {
+            const double p = c0 + lane < m ? P[c0 + lane] : 0.0;
+            const int cn = static_cast<int>(min(64u, m - c0));
+            for (int q = 0; q < cn; ++q) total += readlane_f64(p, q);
+        }
         if (total <= 0.0) {
-            sm.status = kZeroMass;
+            if (lane == 0) sm.status = kZeroMass;
         } else {
-            sm.status = kOk;
+            if (lane == 0) sm.status = kOk;
             const double threshold = 1.0 - static_cast<double>(top_p);
             double cumulative = 0.0;
-            for (uint32_t q = 0; q < m; ++q) {
-                const uint32_t j = static_cast<uint32_t>(sm.sortbuf[q]);
-                cumulative += P[j] / total;
-                if (cumulative <= threshold) sm.list[j] |= kRemoved;
+            for (uint32_t c0 = 0; c0 < m; c0 += 64) {
+                const uint32_t q = c0 + lane;
+                const uint32_t j = q < m ? static_cast<uint32_t>(sm.sortbuf[q]) : 0u;
+                const double r = q < m ? P[j] / total : 0.0;
+                const int cn = static_cast<int>(min(64u, m - c0));
+                uint64_t removed = 0;
+                for (int qq = 0; qq < cn; ++qq) {
+                    cumulative += readlane_f64(r, qq);
+                    if (cumulative <= threshold) removed |= 1ull << qq;
+                }
+                if (q < m && ((removed >> lane) & 1ull)) sm.list[j] |= kRemoved;
             }
             const uint32_t keep = min(m, beams > 1 ? 2u : 1u);
-            for (uint32_t q = m - keep; q < m; ++q) sm.list[static_cast<uint32_t>(sm.sortbuf[q])] &= ~kRemoved;
+            if (static_cast<uint32_t>(lane) < keep) {
+                const uint32_t q = m - keep + lane;
+                sm.list[static_cast<uint32_t>(sm.sortbuf[q])] &= ~kRemoved;
+            }
         }
     }
     __syncthreads();
@@ -324,12 +382,22 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
     return kOk;
 }
 
-// gpt_sampling.cpp:130-165 by thread 0 over the survivors sm.list[0..m) with weights P.
-// Returns the token, or 0xffffffff with *status set when the mass is zero.
-__device__ inline uint32_t draw_token(const Smem& sm, uint32_t m, const double* P, uint64_t& rng, uint32_t* status) {
+// gpt_sampling.cpp:130-165 over the survivors sm.list[0..m) with weights P, run by the 64
+// lanes of one wave (every lane returns the same token): the total over the survivors in
+// index order, target = u * total, then the first survivor whose cumulative mass exceeds
+// the target, else the last one with positive mass.  Both sums run lane-serially in index
+// order.  Returns the token, or 0xffffffff with *status set when the mass is zero.
+__device__ inline uint32_t draw_token_wave(const Smem& sm, uint32_t m, const double* P, uint64_t& rng, uint32_t* status) {
+    const int lane = threadIdx.x & 63;
     double total = 0.0;
-    for (uint32_t j = 0; j < m; ++j)
-        if (!(sm.list[j] & kRemoved)) total += P[j];
+    for (uint32_t c0 = 0; c0 < m; c0 += 64) {
+        const bool in = c0 + lane < m;
+        const double p = in && !(sm.list[c0 + lane] & kRemoved) ? P[c0 + lane] : 0.0;
+        const uint32_t live = static_cast<uint32_t>(in && !(sm.list[c0 + lane] & kRemoved));
+        const int cn = static_cast<int>(min(64u, m - c0));
+        for (int q = 0; q < cn; ++q)
+            if (readlane_u32(live, q)) total += readlane_f64(p, q);
+    }
     if (total <= 0.0) {
         *status = kZeroMass;
         return 0xffffffffu;
@@ -337,14 +405,20 @@ __device__ inline uint32_t draw_token(const Smem& sm, uint32_t m, const double* 
     const double target = splitmix_unit(rng) * total;
     double cumulative = 0.0;
     uint32_t last_finite = 0;
-    for (uint32_t j = 0; j < m; ++j) {
-        const uint16_t e = sm.list[j];
-        if (e & kRemoved) continue;
-        const double p = P[j];
-        if (p <= 0.0) continue;
-        last_finite = e;
-        cumulative += p;
-        if (target < cumulative) return e;
+    for (uint32_t c0 = 0; c0 < m; c0 += 64) {
+        const bool in = c0 + lane < m;
+        const uint32_t e = in ? sm.list[c0 + lane] : static_cast<uint32_t>(kRemoved);
+        const double p = in ? P[c0 + lane] : 0.0;
+        const int cn = static_cast<int>(min(64u, m - c0));
+        for (int q = 0; q < cn; ++q) {
+            const uint32_t eq = readlane_u32(e, q);
+            if (eq & kRemoved) continue;
+            const double pq = readlane_f64(p, q);
+            if (pq <= 0.0) continue;
+            last_finite = eq;
+            cumulative += pq;
+            if (target < cumulative) return eq;
+        }
     }
     return last_finite;
 }

@@ -2,14 +2,16 @@
 //
 // beam_scores_kernel, one 1024-thread workgroup per parent beam:
 //   log_probs = logits - (peak + log(sum_i exp(logit_i - peak)))   (:207-210, float; the
-//   sum is formed by one thread in index order, exp/log evaluated in double and rounded,
-//   i.e. correctly rounded except on double-rounding ties), then the processors with the
+//   sum is formed by one lane in index order from 16-byte LDS reads issued a chunk ahead,
+//   exp/log evaluated in double and rounded, i.e. correctly rounded except on
+//   double-rounding ties), then the processors with the
 //   parent's repetition set (:211-212), then + the parent's beam score (:213).
 // beam_select_kernel, one workgroup:
 //   greedy: the take = 2*beams best of all parents' scores by (score desc, index asc)
 //   (std::partial_sort with index ties, :223-227); sampled: take draws without
-//   replacement with sample_gpt_token_from_logits (:217-222); then a stable sort of the
-//   candidates by score (:228).
+//   replacement with sample_gpt_token_from_logits (:217-222), by wave 0 alone with the
+//   finite candidates in LDS when there are at most kLdsCands of them (each draw's sums
+//   lane-serial in index order); then a stable sort of the candidates by score (:228).
 // The host reads the candidates and runs the reference's child/finish bookkeeping.
 #include "sampler_dev.h"
 
@@ -26,13 +28,24 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     __shared__ float log_sum_s;
     const int p = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float* lg = a.logits + static_cast<size_t>(p) * V;
-    float* e = reinterpret_cast<float*>(sm.sortbuf) + V;  // after s[] inside the union
+    float* e = reinterpret_cast<float*>(sm.sortbuf) + V + 2;  // after s[] inside the union, 16-byte aligned
     float mloc = -INFINITY;
-    for (int i = t; i < V; i += NT) {
-        float v = lg[i];
-        if (a.suppress_stop && (i == kMelStart || i == kMelStop)) v = -INFINITY;
-        sm.s[i] = v;
-        mloc = fmaxf(mloc, v);
+    {
+        float v[IPT];  // all loads in flight before the first store
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            v[q] = i < V ? lg[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V) {
+                const float x = a.suppress_stop && (i == kMelStart || i == kMelStop) ? -INFINITY : v[q];
+                sm.s[i] = x;
+                mloc = fmaxf(mloc, x);
+            }
+        }
     }
     mloc = wave_max(mloc);
     if (lane == 0) wred[wave] = mloc;
@@ -42,8 +55,38 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     for (int i = t; i < V; i += NT) e[i] = expf_cr(sm.s[i] - peak);
     __syncthreads();
     if (t == 0) {
+        // sum += e[0], e[1], ... in index order; the next 16 values are read while the
+        // current 16 are added
+        constexpr int kQuads = V / 4;  // 2048: 8192 values, then the last V % 4
+        static_assert(kQuads % 8 == 0, "two chunks of four quads per iteration");
+        const float4* e4 = reinterpret_cast<const float4*>(e);
         float sum = 0.0f;
-        for (int i = 0; i < V; ++i) sum += e[i];
+        float4 c0[4], c1[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c0[k] = e4[k];
+        for (int q0 = 0; q0 < kQuads; q0 += 8) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c1[k] = e4[q0 + 4 + k];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sum += c0[k].x;
+                sum += c0[k].y;
+                sum += c0[k].z;
+                sum += c0[k].w;
+            }
+            if (q0 + 8 < kQuads) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) c0[k] = e4[q0 + 8 + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sum += c1[k].x;
+                sum += c1[k].y;
+                sum += c1[k].z;
+                sum += c1[k].w;
+            }
+        }
+        for (int i = kQuads * 4; i < V; ++i) sum += e[i];
         log_sum_s = peak + logf_cr(sum);
     }
     __syncthreads();
@@ -132,8 +175,60 @@ __device__ uint32_t block_scan(uint32_t c, uint32_t* wtot, uint32_t* total) {
     return off + inc - c;
 }
 
+// Sampled candidate selection for sampled beams when at most kLdsCands scores are
+// finite, by wave 0 with the candidates in LDS: take draws without replacement, each
+// (gpt_sampling.cpp:130-165 on the remaining candidates) with its maximum, its total and
+// its cumulative scan in index order.  The weights exp(double(score - max)) are recomputed
+// per pass (the same values).  Returns kOk or the failing status; ids[0..take) on success.
+constexpr int kLdsCands = 2048;
+__device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, uint32_t F, int take, uint64_t& rng, uint32_t* ids) {
+    const int lane = threadIdx.x & 63;
+    constexpr uint32_t kTaken = 0x80000000u;
+    for (int d = 0; d < take; ++d) {
+        float m = -INFINITY;  // max over the still-available entries
+        for (uint32_t j = lane; j < F; j += 64)
+            if (!(lid[j] & kTaken)) m = fmaxf(m, lsc[j]);
+        m = wave_max(m);
+        if (m == -INFINITY) return kNoFinite;
+        double total = 0.0;
+        for (uint32_t c0 = 0; c0 < F; c0 += 64) {
+            const uint32_t j = c0 + lane;
+            const double p = j < F && !(lid[j] & kTaken) ? exp(static_cast<double>(lsc[j] - m)) : 0.0;
+            const int cn = static_cast<int>(min(64u, F - c0));
+            for (int q = 0; q < cn; ++q) total += readlane_f64(p, q);
+        }
+        if (total <= 0.0) return kZeroMass;
+        const double target = splitmix_unit(rng) * total;
+        double cumulative = 0.0;
+        uint32_t pick = 0xffffffffu, last = 0xffffffffu;
+        for (uint32_t c0 = 0; c0 < F && pick == 0xffffffffu; c0 += 64) {
+            const uint32_t j = c0 + lane;
+            const double p = j < F && !(lid[j] & kTaken) ? exp(static_cast<double>(lsc[j] - m)) : 0.0;
+            const int cn = static_cast<int>(min(64u, F - c0));
+            for (int q = 0; q < cn; ++q) {
+                const double pq = readlane_f64(p, q);
+                if (pq <= 0.0) continue;
+                last = c0 + static_cast<uint32_t>(q);
+                cumulative += pq;
+                if (target < cumulative) {
+                    pick = last;
+                    break;
+                }
+            }
+        }
+        if (pick == 0xffffffffu) pick = last;
+        if (lane == 0) {
+            ids[d] = lid[pick];
+            lid[pick] |= kTaken;
+        }
+    }
+    return kOk;
+}
+
 __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     __shared__ uint32_t hist[256], sel[2], wtot[NWAVE];
+    __shared__ uint32_t lid[kLdsCands];
+    __shared__ float lsc[kLdsCands];
     __shared__ uint32_t ids[2 * kMaxBeamTake];
     __shared__ float wmax[NWAVE];
     __shared__ float mx_s;
@@ -182,6 +277,43 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
         for (int i = i0; i < i1; ++i) c += finite_f(S[i]);
         uint32_t F = 0;
         uint32_t off = block_scan(c, wtot, &F);
+        if (F <= static_cast<uint32_t>(kLdsCands)) {
+            for (int i = i0; i < i1; ++i) {
+                const float v = S[i];
+                if (finite_f(v)) {
+                    lid[off] = static_cast<uint32_t>(i);
+                    lsc[off] = v;
+                    ++off;
+                }
+            }
+            __syncthreads();
+            if (wave != 0) return;
+            uint64_t rng = *a.rng;
+            const uint32_t st = draw_candidates_wave(lid, lsc, F, take, rng, ids);
+            if (st != kOk) {
+                if (t == 0) a.status[0] = st;
+                return;
+            }
+            if (t == 0) {
+                *a.rng = rng;
+                // Stable sort by score, descending (std::sort on <= 16 candidates is an insertion sort).
+                for (int x = 1; x < take; ++x) {
+                    const uint32_t v = ids[x];
+                    int y = x - 1;
+                    while (y >= 0 && S[ids[y]] < S[v]) {
+                        ids[y + 1] = ids[y];
+                        --y;
+                    }
+                    ids[y + 1] = v;
+                }
+                a.status[0] = kOk;
+            }
+            if (t < take) {
+                const uint32_t id = ids[t];
+                a.cand[t] = BeamCand{id / static_cast<uint32_t>(V), id % static_cast<uint32_t>(V), S[id], 0u};
+            }
+            return;
+        }
         for (int i = i0; i < i1; ++i)
             if (finite_f(S[i])) a.list[off++] = static_cast<uint32_t>(i);
         __syncthreads();

@@ -151,6 +151,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs)")
     ap.add_argument("--iters", type=int, default=240)
+    ap.add_argument("--kernel-batch", type=int, default=1, help="sequences per launch for --kernel-only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
@@ -161,8 +162,9 @@ def main() -> int:
     weights = it.make_synthetic_weights(layers=24, seed=0)
     dec = it.GptDecoder(weights, kv_capacity=4096, max_batch=8)
     if args.kernel_only:
-        k = dec.bench_kernel(args.kernel_only, iters=args.iters)
-        print(json.dumps({"kernel": args.kernel_only, "iters": args.iters, "avg_us": round(k["avg_ms"] * 1e3, 3),
+        k = dec.bench_kernel(args.kernel_only, iters=args.iters, batch=args.kernel_batch)
+        print(json.dumps({"kernel": args.kernel_only, "batch": args.kernel_batch, "iters": args.iters,
+                          "avg_us": round(k["avg_ms"] * 1e3, 3),
                           "bytes_per_launch": k["bytes"], "GBps": round(k["bytes"] / (k["avg_ms"] * 1e-3) / 1e9, 1)}),
               flush=True)
         return 0

@@ -114,10 +114,20 @@ struct StepArgs {
     float* logits;            // [8194]
     uint32_t epoch;           // tag base of this launch (fresh per launch, never 0)
     uint32_t* err;            // set to 1 when a hand-off wait gives up
+    // batch step (step_batch.hip): sequences state[0..nseq), KV slots kv + q * kv_slot_stride,
+    // logits rows logits + q * logit_stride, exchange regions xch + q * kStepExchangeTotal
+    int nseq;
+    size_t kv_slot_stride;
+    int logit_stride;
 };
 bool step_fits(int grid);
 hipError_t step_occupancy(bool bf16, int* blocks_per_cu);
 hipError_t launch_step(const StepArgs& a, int grid, bool bf16, hipStream_t s);
+// Persistent step for 2..kStepBatchMax sequences (FP32 weights, no beam row-owner table).
+constexpr int kStepBatchMax = 4;
+bool step_batch_fits(int grid, int nseq);
+hipError_t step_batch_occupancy(int nseq, int* blocks_per_cu);
+hipError_t launch_step_batch(const StepArgs& a, int nseq, int grid, hipStream_t s);
 
 // ------------------------------------------------------------------ sampler
 enum SampleMode : int {

@@ -89,7 +89,7 @@ struct Snapshot {
 // this process on different streams) could each hold CUs the other is waiting for, so
 // the launches on a device are chained: each waits for the previous one, whichever decoder
 // made it.  The chain is process-wide and never freed.
-hipError_t launch_step_serialized(const StepArgs& a, int grid, bool bf16, int dev, hipStream_t s) {
+hipError_t launch_step_serialized(const StepArgs& a, int nseq, int grid, bool bf16, int dev, hipStream_t s) {
     static std::mutex mu;
     static std::unordered_map<int, hipEvent_t> last;  // device -> recorded after its latest step launch
     std::lock_guard<std::mutex> lock(mu);
@@ -103,7 +103,7 @@ hipError_t launch_step_serialized(const StepArgs& a, int grid, bool bf16, int de
         const hipError_t err = hipStreamWaitEvent(s, it->second, 0);
         if (err != hipSuccess) return err;
     }
-    const hipError_t err = launch_step(a, grid, bf16, s);
+    const hipError_t err = nseq == 1 ? launch_step(a, grid, bf16, s) : launch_step_batch(a, nseq, grid, s);
     if (err != hipSuccess) return err;
     return hipEventRecord(it->second, s);
 }
@@ -151,6 +151,7 @@ struct Engine {
     // Persistent single-sequence step (step.hip): one launch per token for batch-1 decode
     // (bitwise the same logits as the multi-kernel path, which ITTS_GPT_PERSISTENT=0 selects).
     bool step_ok = false;
+    bool step_batch_ok[kStepBatchMax + 1] = {};  // persistent batch step available for this many sequences
     int step_grid = 0;
     int step_dev = 0;
     size_t per_layer = 0;       // weight elements per layer block
@@ -346,7 +347,16 @@ struct Engine {
         HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         HIP_CHECK(step_occupancy(false, &occ));
         if (occ < 1 || !step_fits(cus)) return;
-        xch.alloc(kStepExchangeTotal);
+        // Batches of 2..4 sequences per launch (step_batch.hip), opt-in with
+        // ITTS_GPT_PERSISTENT_BATCH=1: it does not yet beat the multi-kernel path at batch > 1.
+        const char* pb = std::getenv("ITTS_GPT_PERSISTENT_BATCH");
+        const bool batch = max_batch >= 2 && pb && std::strcmp(pb, "1") == 0;
+        for (int nb = 2; batch && nb <= kStepBatchMax; ++nb) {
+            int bocc = 0;
+            HIP_CHECK(step_batch_occupancy(nb, &bocc));
+            step_batch_ok[nb] = bocc >= 1 && step_batch_fits(cus, nb);
+        }
+        xch.alloc(kStepExchangeTotal * (batch ? kStepBatchMax : 1));
         HIP_CHECK(hipMemsetAsync(xch.p, 0, xch.n * sizeof(uint64_t), stream));
         step_err.alloc(1);
         HIP_CHECK(hipMemsetAsync(step_err.p, 0, sizeof(uint32_t), stream));
@@ -354,7 +364,9 @@ struct Engine {
         step_ok = true;
     }
 
-    StepArgs step_args() {
+    // Arguments of one persistent step launch for sequences q0 .. q0 + nq - 1 (slots, states and
+    // logits rows from q0; each launch takes its own range of tags).
+    StepArgs step_args(int q0 = 0, int nq = 1) {
         // Each launch takes a fresh range of 8*(layers+1) tags; before the 32-bit counter
         // wraps, the exchange is cleared and numbering restarts.
         const uint32_t span = 8u * static_cast<uint32_t>(layers + 1);
@@ -370,17 +382,20 @@ struct Engine {
         s.head = head_params.p;
         s.mel_emb = mel_emb.p;
         s.mel_pos = mel_pos.p;
-        s.kv = kv.p;
+        s.kv = kv.p + static_cast<size_t>(q0) * kv_slot_stride;
         s.kv_layer_stride = kv_layer_stride;
         s.kv_v_off = kv_v_off;
         s.kv_cap = cap;
         s.layers = layers;
         s.splits = splits;
-        s.state = state.p;
+        s.state = state.p + q0;
         s.xch = xch.p;
-        s.logits = logits.p;
+        s.logits = logits.p + static_cast<size_t>(q0) * kMelVocab;
         s.epoch = epoch;
         s.err = step_err.p;
+        s.nseq = nq;
+        s.kv_slot_stride = kv_slot_stride;
+        s.logit_stride = kMelVocab;
         epoch += span;
         return s;
     }
@@ -395,7 +410,20 @@ struct Engine {
             throw std::runtime_error("GPT decode step: a workgroup hand-off timed out");
         }
     }
-    bool persistent(int nseq, bool use_table) const { return step_ok && nseq == 1 && !use_table; }
+    // The persistent path covers nseq sequences in launches of up to kStepBatchMax (the last
+    // launch takes the remainder; one sequence goes to the batch-1 step).
+    bool persistent(int nseq, bool use_table) const {
+        if (!step_ok || use_table || nseq < 1) return false;
+        if (nseq == 1) return true;
+        const int rem = nseq % kStepBatchMax;
+        return (nseq < kStepBatchMax || step_batch_ok[kStepBatchMax]) && (rem < 2 || step_batch_ok[rem]);
+    }
+    void launch_persistent(int nseq) {
+        for (int q0 = 0; q0 < nseq; q0 += kStepBatchMax) {
+            const int nq = std::min(kStepBatchMax, nseq - q0);
+            HIP_CHECK(launch_step_serialized(step_args(q0, nq), nq, step_grid, bf16, step_dev, stream));
+        }
+    }
 
     // ---------------------------------------------------------------- forward pieces
     GemvArgs gemv_base(int nseq) const {
@@ -514,7 +542,7 @@ struct Engine {
     void run_step(int nseq, int nb, bool sampler, bool use_table) {
         if (persistent(nseq, use_table)) {
             timing.decode_path = ITTS_PATH_STEP;
-            HIP_CHECK(launch_step_serialized(step_args(), step_grid, bf16, step_dev, stream));
+            launch_persistent(nseq);
             if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
             return;
         }
@@ -931,7 +959,7 @@ struct Engine {
     void bench_kernel(int which, int batch, uint32_t cached_rows, int iters, float* avg_ms, double* bytes) {
         if (!layers || which < 0 || which > 7 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
             throw std::invalid_argument("Invalid kernel benchmark request");
-        if (which == 6 && (!step_ok || batch != 1)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
+        if (which == 6 && !persistent(batch, false)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
         if (!cached_rows) cached_rows = 752;
         if (cached_rows + 1 >= cap) throw std::invalid_argument("Invalid kernel benchmark request");
         if (which == 7) {
@@ -979,7 +1007,7 @@ struct Engine {
                     enqueue_head(batch, nb);
                     break;
                 case 6:
-                    HIP_CHECK(launch_step_serialized(step_args(), step_grid, bf16, step_dev, stream));
+                    launch_persistent(batch);
                     break;
                 default: {
                     AttnArgs t{};
@@ -1001,9 +1029,10 @@ struct Engine {
         const double rows[5] = {kQkv, kWidth, kFfn, kWidth, kMelVocab};
         const double cols[5] = {kWidth, kWidth, kWidth, kFfn, kWidth};
         if (which == 6) {
-            // the whole forward: every weight byte once + K/V rows read and the new row written
-            const double weights = static_cast<double>(slab.n) + 4.0 * (params.n + head_params.n) + 2.0 * kWidth * 4;
-            *bytes = weights + static_cast<double>(layers) * 2.0 * (st[0].n + 1) * kWidth * 4.0;
+            // the whole forward: every weight byte once, then per sequence its embedding rows and
+            // K/V rows read and the new row written
+            const double weights = static_cast<double>(slab.n) + 4.0 * (params.n + head_params.n);
+            *bytes = weights + batch * (2.0 * kWidth * 4 + static_cast<double>(layers) * 2.0 * (st[0].n + 1) * kWidth * 4.0);
             check_step_error();
         } else if (which < 5) {
             // weights + bias + input rows (+ LayerNorm params) + outputs, per launch

@@ -1,0 +1,862 @@
+// Persistent decode step for B = 2..4 sequences at once (batched requests): the batch-1
+// step kernel's structure (step.hip) with every activation vector, attention tile, merge,
+// residual and logits row per sequence, and the weights streamed once for all of them.
+//
+// What is per sequence q:
+//   * the exchange: sequence q owns a whole batch-1 exchange layout at q * kStepExchangeTotal
+//     (broadcast copies included), tagged with the launch's epochs;
+//   * the KV cache of slot q (kv + q * kv_slot_stride), its cached length n_q and its
+//     attention tiles: the tile list is sequence 0's 20 x S_0 tiles, then sequence 1's, ...,
+//     dealt to workgroups round by round as in step.hip; the merge of (q, head h) runs on
+//     workgroup 20 q + h;
+//   * the logits row (logits + q * logit_stride) and the decode state (state[q]).
+// A workgroup's GEMV rows are the same as in step.hip; each row group's weights are read
+// from the LDS ring once and multiplied with the B input vectors (B FMA chains, each in the
+// batch-1 order and reduced with the batch-1 pairings), so every sequence's logits are
+// bitwise those of a batch-1 step.
+//
+// LDS: the phase inputs of all B sequences share one staging area (B x 5120 floats), so
+// the ring is smaller than step.hip's (22, 18, 14 chunks for B = 2, 3, 4) and row groups
+// span at most ring - 1 chunks.  Rows go in groups of four and 5120-wide rows one at a time
+// (step.hip's five-row groups and row pairs need more registers than B inputs leave).  A GEMV's input rows stay in LDS (a LayerNorm phase writes the
+// normalised row next to the raw one) and are read 16 bytes per lane per piece, so the
+// registers hold only the row group's weights and B accumulators.  Since consecutive phases
+// reuse the staging area, each phase ends its reads of it at a compute-wave barrier before
+// the next phase writes.
+//
+// Reference ops replaced: gpt.cpp:88-125 for several step rows (as step.hip), the batched
+// form of the reference's per-row GEMV (kernels.metal mit2_linear_gemv_f32 :1054-1080).
+#include "step_common.h"
+
+namespace itts {
+namespace {
+using namespace stepc;
+
+template <int B>
+struct BCfg {
+    static_assert(B >= 2 && B <= kStepBatchMax, "batch of the persistent batch step");
+    static constexpr int kRing = B == 2 ? 22 : B == 3 ? 18 : 14;
+    static constexpr bool kFive = false;        // five-row groups (17 chunks) need more registers than B inputs leave
+    static constexpr bool kPairs = false;       // 5120-wide rows one at a time (pairs need more registers)
+};
+constexpr int kResidMax = 16;  // own rows of attn.c_proj / mlp.c_proj per workgroup (grid >= 80)
+
+// Exchange region of sequence q (a batch-1 layout).
+__device__ __forceinline__ uint64_t* xregion(uint64_t* x, int q) { return x + static_cast<size_t>(q) * kStepExchangeTotal; }
+
+// Value a[q] of a small register array, as a chain of selects.  Each element passes through
+// an empty asm: otherwise the compiler turns the chain back into an indexed load, which puts
+// the whole array in scratch memory.
+template <int B>
+__device__ __forceinline__ int pick(const int (&a)[B], int q) {
+    int v = a[0];
+#pragma unroll
+    for (int i = 1; i < B; ++i) {
+        int ai = a[i];
+        asm volatile("" : "+v"(ai));
+        v = q == i ? ai : v;
+    }
+    return v;
+}
+
+// This workgroup's share of the step, identical in every wave.
+template <int B>
+struct PlanB {
+    int G, b;
+    int n[B], L[B], S[B], chunk_rows[B], tiles[B];  // per sequence: cached rows, keys, splits, rows per split, tiles
+    int active[B];                                   // per sequence: still decoding (its K/V row is appended)
+    int ntiles, rounds;
+    int q0, qn, p0, pn, f0, fn, g0, gn, h0, hn;  // row slices: c_attn, c_proj, c_fc, mlp.c_proj, mel_head
+    int att_chunks, layer_chunks;
+    int o_att, o_proj, o_fc, o_fc2;
+
+    __device__ static void slice(int rows, int G, int b, int& r0, int& cnt) {
+        const int per = (rows + G - 1) / G;
+        r0 = b * per;
+        cnt = max(0, min(per, rows - r0));
+    }
+    // Attention tile of round rd: sequence sq, head h, split s, first row t0, cached rows R.
+    __device__ __forceinline__ bool tile(int rd, int& sq, int& h, int& s, int& t0, int& R) const {
+        int t = b + G * rd;
+        if (t >= ntiles) return false;
+        sq = 0;
+#pragma unroll
+        for (int q = 0; q + 1 < B; ++q)
+            if (sq == q && t >= tiles[q]) {
+                t -= tiles[q];
+                sq = q + 1;
+            }
+        h = t % kHeads;
+        s = t / kHeads;
+        const int cr = pick(chunk_rows, sq);
+        t0 = s * cr;
+        const int t1 = min(pick(L, sq), t0 + cr);
+        R = max(0, min(t1, pick(n, sq)) - t0);
+        return true;
+    }
+    __device__ __forceinline__ static int kv_chunks(int R) { return (R + kKvRowsPerChunk - 1) / kKvRowsPerChunk; }
+
+    __device__ __forceinline__ void init(const SeqState* st, int splits) {
+        G = static_cast<int>(gridDim.x);
+        b = static_cast<int>(blockIdx.x);
+        ntiles = 0;
+#pragma unroll
+        for (int q = 0; q < B; ++q) {
+            n[q] = static_cast<int>(st[q].n);
+            active[q] = st[q].active != 0;
+            L[q] = n[q] + 1;
+            S[q] = live_splits_dev(L[q], splits);
+            chunk_rows[q] = (L[q] + S[q] - 1) / S[q];
+            tiles[q] = kHeads * S[q];
+            ntiles += tiles[q];
+        }
+        rounds = (ntiles + G - 1) / G;
+        slice(kQkv, G, b, q0, qn);
+        slice(kWidth, G, b, p0, pn);
+        slice(kFfn, G, b, f0, fn);
+        slice(kWidth, G, b, g0, gn);
+        slice(kMelVocab, G, b, h0, hn);
+        att_chunks = 0;
+        for (int rd = 0; rd < rounds; ++rd) {
+            int sq, h, s, t0, R;
+            if (tile(rd, sq, h, s, t0, R)) att_chunks += 2 * kv_chunks(R);
+        }
+        o_att = qn;
+        o_proj = o_att + att_chunks;
+        o_fc = o_proj + pn;
+        o_fc2 = o_fc + fn;
+        layer_chunks = o_fc2 + 4 * gn;
+    }
+};
+
+template <int B>
+struct SmemB {
+    union {
+        float stage[B][kFfn];                       // the phase's inputs, per sequence
+        float mpart[kAttnMaxSplits][2 + kHeadDim];  // gathered attention partials of one head (merge)
+    };
+    float resid_h[B][kResidMax];  // h at this workgroup's attn.c_proj rows (their residual)
+    float resid_m[B][kResidMax];  // hmid at this workgroup's mlp.c_proj rows
+    float redm[4], reds[4];
+    float accs[16][kHeadDim + 4];
+};
+
+// ------------------------------------------------------------------ loader waves
+
+// chunk_src of step.hip with the tiles of several sequences: a K/V chunk reads sequence sq's
+// cache slot.
+template <int B>
+__device__ __forceinline__ void chunk_src_b(const StepArgs& a, const PlanB<B>& P, const float* W, int l, int r, int lane,
+                                            const float*& base, uint32_t& extent, uint32_t (&off)[kLines]) {
+    if (l >= a.layers) {
+        base = W + a.off_head + static_cast<size_t>(P.h0 + r) * kWidth;
+    } else {
+        const float* wl = W + static_cast<size_t>(l) * a.layer_stride;
+        if (r < P.o_att) {
+            base = wl + static_cast<size_t>(P.q0 + r) * kWidth;
+        } else if (r < P.o_proj) {
+            int q = r - P.o_att, sq = 0, h = 0, s = 0, t0 = 0, R = 0, kc = 0;
+            for (int rd = 0; rd < P.rounds; ++rd) {
+                if (!P.tile(rd, sq, h, s, t0, R)) continue;
+                kc = PlanB<B>::kv_chunks(R);
+                if (q < 2 * kc) break;
+                q -= 2 * kc;
+            }
+            const bool is_v = q >= kc;
+            const int j = is_v ? q - kc : q;
+            const float* kvb = a.kv + static_cast<size_t>(sq) * a.kv_slot_stride + static_cast<size_t>(l) * a.kv_layer_stride +
+                               (is_v ? a.kv_v_off : 0) + static_cast<size_t>(h) * a.kv_cap * kHeadDim;
+            base = kvb + static_cast<size_t>(t0) * kHeadDim;
+            extent = static_cast<uint32_t>(R) * kHeadDim * 4;
+#pragma unroll
+            for (int k = 0; k < kLines; ++k) {
+                int row = kKvRowsPerChunk * j + 4 * k + (lane >> 4);  // tile-local row
+                if (row >= R) row = 0;                                 // clamped: loaded, never read
+                off[k] = static_cast<uint32_t>((row * kHeadDim + (lane & 15) * 4) * 4);
+            }
+            return;
+        } else if (r < P.o_fc) {
+            base = wl + static_cast<size_t>(kQkv) * kWidth + static_cast<size_t>(P.p0 + r - P.o_proj) * kWidth;
+        } else if (r < P.o_fc2) {
+            base = wl + static_cast<size_t>(kQkv + kWidth) * kWidth + static_cast<size_t>(P.f0 + r - P.o_fc) * kWidth;
+        } else {
+            const int q = r - P.o_fc2;
+            base = wl + static_cast<size_t>(kQkv + kWidth + kFfn) * kWidth + static_cast<size_t>(P.g0 + (q >> 2)) * kFfn +
+                   (q & 3) * kChunkF;
+        }
+    }
+    extent = kChunkF * 4;
+#pragma unroll
+    for (int k = 0; k < kLines; ++k) off[k] = static_cast<uint32_t>((k * 256 + lane * 4) * 4);
+}
+
+// ------------------------------------------------------------------ compute waves
+
+// dst = LayerNorm(row) for this thread's 5 columns (tid + 256 i); the statistics are those of
+// ln_stats (every wave forms them for the whole row), so the values equal ln_to_xrow's.
+__device__ __forceinline__ void ln_rows_to(const float* row, float* dst, const LnPar& p, int tid, int lane) {
+    float v[4][5], mean, inv;
+    ln_layout_load(row, lane, v);
+    ln_stats(v, mean, inv);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) dst[tid + 256 * i] = ln_apply(row[tid + 256 * i], mean, inv, p.g[i], p.b[i]);
+}
+
+// rowsN of step.hip for B inputs: rows k0 + 4 t (t < N, those below cnt) of a 1280-wide slice,
+// each multiplied with every sequence's input row xs[q] (in LDS, read 16 bytes per lane per
+// piece j as the batch-1 XRow holds it); res[q] as wave_sum4 leaves it (row k0 + 4 t in lanes
+// 0-15, 32-47, 16-31, 48-63 for t = 0..3), fifth[q] the fifth row's sum (N == 5).
+template <int N, int B, int RING>
+__device__ __forceinline__ void rowsNB(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const float* const (&xs)[B], int wave,
+                                       int lane, uint32_t* err, bool& failed, float (&res)[B], float (&fifth)[B]) {
+    static_assert(N == 4 || N == 5, "row group size");
+    release_to(ctl, c0 + k0, wave);
+    const int nt = N == 5 ? 5 : min(4, (cnt - k0 + 3) >> 2);
+    (void)wait_chunk<RING>(ctl, ring, c0 + k0 + 4 * (nt - 1), err, failed);
+    const float* ch[N];
+#pragma unroll
+    for (int t = 0; t < N; ++t) ch[t] = ring + ((c0 + k0 + 4 * (t < nt ? t : 0)) % RING) * kChunkF;  // absent rows re-read row k0
+    float4 w[N][5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j)
+#pragma unroll
+        for (int t = 0; t < N; ++t) w[t][j] = *reinterpret_cast<const float4*>(ch[t] + (j * 64 + lane) * 4);
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[N][B];
+#pragma unroll
+    for (int t = 0; t < N; ++t)
+#pragma unroll
+        for (int q = 0; q < B; ++q) acc[t][q] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        float4 x[B];
+#pragma unroll
+        for (int q = 0; q < B; ++q) x[q] = *reinterpret_cast<const float4*>(xs[q] + (j * 64 + lane) * 4);
+#pragma unroll
+        for (int t = 0; t < N; ++t)
+#pragma unroll
+            for (int q = 0; q < B; ++q) {
+                acc[t][q] = __builtin_fmaf(w[t][j].x, x[q].x, acc[t][q]);
+                acc[t][q] = __builtin_fmaf(w[t][j].y, x[q].y, acc[t][q]);
+                acc[t][q] = __builtin_fmaf(w[t][j].z, x[q].z, acc[t][q]);
+                acc[t][q] = __builtin_fmaf(w[t][j].w, x[q].w, acc[t][q]);
+            }
+    }
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+        if constexpr (N == 5) fifth[q] = wave_sum(acc[4][q]);
+        res[q] = wave_sum4(acc[0][q], acc[1][q], acc[2][q], acc[3][q]);
+    }
+}
+
+// gemv_rows of step.hip for B inputs: out(k, bias, q, sum) in the lane holding row k's sum of
+// sequence q.  Biases come from `bias` for the first NG groups, later from bias_mem.
+template <int B, int RING, bool kFive, int NG, class Out>
+__device__ __forceinline__ void gemv_rows_b(Ctl& ctl, const float* ring, int c0, int cnt, const float* const (&xr)[B], const LaneBias<NG, false>& bias,
+                                            const float* __restrict__ bias_mem, int wave, int lane, uint32_t* err, bool& failed, Out out) {
+    const int t = row_of_lane4(lane);
+    const bool holder = (lane & 15) == 0;
+    int g = 0;
+    for (int k0 = wave; k0 < cnt; k0 += 16, ++g) {
+        const int k = k0 + 4 * t;
+        float b4 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NG; ++i)
+            if (g == i) b4 = bias.v[i];
+        if (g >= NG && holder && k < cnt) b4 = bias_mem[k];
+        float res[B], fifth[B];
+        if (kFive && k0 + 16 < cnt && k0 + 20 >= cnt) {  // exactly five rows left
+            rowsNB<kFive ? 5 : 4, B, RING>(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed, res, fifth);
+            const float b5 = bias_mem[k0 + 16];
+#pragma unroll
+            for (int q = 0; q < B; ++q) {
+                if (holder && k < cnt) out(k, b4, q, res[q]);
+                if (lane == 0) out(k0 + 16, b5, q, fifth[q]);
+            }
+            return;
+        }
+        rowsNB<4, B, RING>(ctl, ring, c0, k0, cnt, xr, wave, lane, err, failed, res, fifth);
+#pragma unroll
+        for (int q = 0; q < B; ++q)
+            if (holder && k < cnt) out(k, b4, q, res[q]);
+    }
+}
+
+// mlp.c_proj rows (5120 wide) for B inputs: rows k0 and, when kPairs, k0 + 4, reduced per
+// sequence with wave_sum2 (pairs: lanes 0 and 32) or wave_sum (single rows: every lane).
+template <int B, int RING, bool kPairs>
+__device__ __forceinline__ void rows_wide_b(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const float (*xs)[kFfn], int wave,
+                                            int lane, uint32_t* err, bool& failed, float (&res)[B]) {
+    const bool two = kPairs && k0 + kCW < cnt;
+    release_to(ctl, c0 + 4 * k0, wave);
+    wait_run4(ctl, c0 + 4 * (two ? k0 + kCW : k0), err, failed);
+    float a0[B], a1[B];
+#pragma unroll
+    for (int q = 0; q < B; ++q) a0[q] = a1[q] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float* r0 = ring + ((c0 + 4 * k0 + m) % RING) * kChunkF;
+        const float* r1 = two ? ring + ((c0 + 4 * (k0 + kCW) + m) % RING) * kChunkF : r0;
+        float4 w0[5], w1[5];
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            w0[j] = *reinterpret_cast<const float4*>(r0 + (j * 64 + lane) * 4);
+            if constexpr (kPairs) w1[j] = *reinterpret_cast<const float4*>(r1 + (j * 64 + lane) * 4);
+        }
+#pragma unroll
+        for (int q = 0; q < B; ++q) {
+            float4 x[5];
+#pragma unroll
+            for (int j = 0; j < 5; ++j) x[j] = *reinterpret_cast<const float4*>(xs[q] + ((5 * m + j) * 64 + lane) * 4);
+#pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                a0[q] = __builtin_fmaf(w0[j].x, x[j].x, a0[q]);
+                a0[q] = __builtin_fmaf(w0[j].y, x[j].y, a0[q]);
+                a0[q] = __builtin_fmaf(w0[j].z, x[j].z, a0[q]);
+                a0[q] = __builtin_fmaf(w0[j].w, x[j].w, a0[q]);
+                if constexpr (kPairs) {
+                    a1[q] = __builtin_fmaf(w1[j].x, x[j].x, a1[q]);
+                    a1[q] = __builtin_fmaf(w1[j].y, x[j].y, a1[q]);
+                    a1[q] = __builtin_fmaf(w1[j].z, x[j].z, a1[q]);
+                    a1[q] = __builtin_fmaf(w1[j].w, x[j].w, a1[q]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < B; ++q) res[q] = kPairs ? wave_sum2(a0[q], a1[q]) : wave_sum(a0[q]);
+}
+
+constexpr int kGQkv = 1, kGProj = 1, kGFc = 2, kGHead = 3;
+constexpr int kMergeRegSplits = 16;
+
+template <int B>
+__global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
+    using C = BCfg<B>;
+    constexpr int RING = C::kRing;
+    __shared__ float ring[RING * kChunkF];
+    __shared__ Ctl ctl;
+    __shared__ SmemB<B> sm;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        bool any = false;
+#pragma unroll
+        for (int q = 0; q < B; ++q) any |= a.state[q].active != 0;
+        if (!any) return;
+    }
+    if (tid < kLW) ctl.done[tid] = 0;
+    if (tid < kCW) ctl.need[tid] = 0;
+    if (tid == 0) ctl.bar = 0;
+    __syncthreads();  // the only barrier of the whole workgroup; roles split below
+
+    PlanB<B> P;
+    P.init(a.state, a.splits);
+    const int total_chunks = a.layers * P.layer_chunks + P.hn;
+
+    // ================================================================ loaders
+    if (wave >= kCW) {
+        const float* __restrict__ W = static_cast<const float*>(a.w);
+        const int lw = __builtin_amdgcn_readfirstlane(wave - kCW);
+        run_loader<RING>(a, P.layer_chunks, P.hn, ring, ctl, lw, lane,
+                         [&](int l, int r, const float*& base, uint32_t& extent, uint32_t(&off)[kLines]) {
+                             chunk_src_b<B>(a, P, W, l, r, lane, base, extent, off);
+                         });
+        return;
+    }
+
+    // ================================================================ compute waves
+    bool failed = false;
+    uint32_t gen = 0;
+    const int cpy = P.b % kStepCopies;
+    const uint32_t e0 = a.epoch;
+    auto ep = [&](int l, uint32_t kind) { return e0 + 8u * static_cast<uint32_t>(l) + kind; };
+    auto XW = [&](int q) { return xregion(a.xch, q); };                                  // written by producers
+    auto XR = [&](int q) -> const uint64_t* { return xregion(a.xch, q) + xcopy(cpy, 0); };  // this workgroup's copy
+
+    for (int l = 0; l < a.layers; ++l) {
+        const float* __restrict__ par = a.params + static_cast<size_t>(l) * kParLayer;
+        const size_t kvl = static_cast<size_t>(l) * a.kv_layer_stride;
+        const int cb = l * P.layer_chunks;
+
+        // ------------------------------------------------ LN1 + c_attn (+ K/V append)
+        {
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+            release_to(ctl, cb, wave);
+            int idx[5];
+            bool use[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                idx[i] = kXh + tid + 256 * i;
+                use[i] = l > 0;
+            }
+            XRead<5> xr[B];
+#pragma unroll
+            for (int q = 0; q < B; ++q) xr[q].issue(XR(q), idx, use, ep(l, kEpXh));
+            LnPar ln;
+            ln.load(par + kParLn1W, par + kParLn1B, tid);
+            LaneBias<kGQkv, false> bias;
+            bias.load(par + kParQkvB + P.q0, P.qn, wave, lane);
+#pragma unroll
+            for (int q = 0; q < B; ++q) {
+                float hv[5];
+                if (l == 0) {
+                    const SeqState& sq = a.state[q];
+#pragma unroll
+                    for (int i = 0; i < 5; ++i) {
+                        const int c = tid + 256 * i;
+                        hv[i] = a.mel_emb[static_cast<size_t>(sq.token) * kWidth + c] + a.mel_pos[static_cast<size_t>(sq.position) * kWidth + c];
+                    }
+                } else {
+                    xr[q].wait(XR(q), idx, ep(l, kEpXh), hv, a.err, failed);
+                }
+#pragma unroll
+                for (int i = 0; i < 5; ++i) sm.stage[q][tid + 256 * i] = hv[i];
+            }
+            cbar(ctl, gen, a.err, failed);
+            if (wave == 0 && lane < P.pn) {
+#pragma unroll
+                for (int q = 0; q < B; ++q) sm.resid_h[q][lane] = sm.stage[q][P.p0 + lane];
+            }
+#pragma unroll
+            for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q], sm.stage[q] + kWidth, ln, tid, lane);
+            cbar(ctl, gen, a.err, failed);
+            const float* x[B];
+#pragma unroll
+            for (int q = 0; q < B; ++q) x[q] = sm.stage[q] + kWidth;
+            const uint32_t e = ep(l, kEpQkv);
+            auto out = [&](int k, float b, int q, float acc) {
+                const int row = P.q0 + k;
+                const float v = acc + b;
+                xst_bcast(XW(q), kXqkv + row, e, v);
+                if (row >= kWidth && pick(P.active, q)) {
+                    const int rr = row - kWidth;
+                    const bool is_v = rr >= kWidth;
+                    const int c = is_v ? rr - kWidth : rr;
+                    const size_t nrow = static_cast<size_t>(pick(P.n, q));
+                    a.kv[static_cast<size_t>(q) * a.kv_slot_stride + kvl + (is_v ? a.kv_v_off : 0) +
+                         (static_cast<size_t>(c >> 6) * a.kv_cap + nrow) * kHeadDim + (c & 63)] = v;
+                }
+            };
+            gemv_rows_b<B, RING, C::kFive>(ctl, ring, cb, P.qn, x, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
+            stores_done();
+        }
+
+        // ------------------------------------------------ split-KV attention tiles
+        {
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+            const int g = tid >> 4, sub = tid & 15;
+            const uint32_t eq = ep(l, kEpQkv), epart = ep(l, kEpPart);
+            int ca = cb + P.o_att;
+            release_to(ctl, ca, wave);
+            for (int rd = 0; rd < P.rounds; ++rd) {
+                int sq = 0, h = 0, s = 0, t0 = 0, R = 0;
+                const bool act = P.tile(rd, sq, h, s, t0, R);
+                const int nq = act ? pick(P.n, sq) : 0;
+                const int p1 = act ? min(pick(P.L, sq), t0 + pick(P.chunk_rows, sq)) : 0;
+                const int kc = act ? PlanB<B>::kv_chunks(R) : 0;
+                constexpr int PER = kAttnMaxChunk / 16;
+                constexpr int PERL = 4;
+                float4 k4[PER], v4[PER];
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    v4[i] = k4[i];
+                }
+                const int dn = nq - t0 - g;
+                const int i_new = (act && nq < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < PERL) ? (dn >> 4) : -1;
+                int idx[12];
+                bool use[12];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    idx[k] = kXqkv + h * kHeadDim + sub * 4 + k;
+                    idx[4 + k] = kXqkv + kWidth + h * kHeadDim + sub * 4 + k;
+                    idx[8 + k] = kXqkv + 2 * kWidth + h * kHeadDim + sub * 4 + k;
+                    use[k] = act;
+                    use[4 + k] = use[8 + k] = i_new >= 0;
+                }
+                const uint64_t* XQ = XR(act ? sq : 0);
+                XRead<12> xr;
+                xr.issue(XQ, idx, use, eq);
+                for (int j = 0; j < 2 * kc; ++j) (void)wait_chunk<RING>(ctl, ring, ca + j, a.err, failed);
+#pragma unroll
+                for (int i = 0; i < PERL; ++i) {
+                    const int r = g + 16 * i;
+                    if (act && r < R) {
+                        const float* kch = ring + ((ca + r / kKvRowsPerChunk) % RING) * kChunkF;
+                        const float* vch = ring + ((ca + kc + r / kKvRowsPerChunk) % RING) * kChunkF;
+                        const int off = (r % kKvRowsPerChunk) * kHeadDim + sub * 4;
+                        k4[i] = *reinterpret_cast<const float4*>(kch + off);
+                        v4[i] = *reinterpret_cast<const float4*>(vch + off);
+                    }
+                }
+                ca += 2 * kc;
+                release_to(ctl, ca, wave);
+                float4 q4;
+                {
+                    float qv[12];
+                    xr.wait(XQ, idx, eq, qv, a.err, failed);
+                    q4 = make_float4(qv[0], qv[1], qv[2], qv[3]);
+                    const float4 kn = make_float4(qv[4], qv[5], qv[6], qv[7]);
+                    const float4 vn = make_float4(qv[8], qv[9], qv[10], qv[11]);
+#pragma unroll
+                    for (int i = 0; i < PER; ++i) {
+                        if (i == i_new) {
+                            k4[i] = kn;
+                            v4[i] = vn;
+                        }
+                    }
+                }
+                float sc[PER];
+                float mloc = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    float d = q4.x * k4[i].x;
+                    d = __builtin_fmaf(q4.y, k4[i].y, d);
+                    d = __builtin_fmaf(q4.z, k4[i].z, d);
+                    d = __builtin_fmaf(q4.w, k4[i].w, d);
+                    d = sum16_up(d);
+                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
+                    sc[i] = valid ? d * 0.125f : -INFINITY;
+                    mloc = fmaxf(mloc, sc[i]);
+                }
+                const float wm = wave_max(mloc);
+                if (lane == 0) sm.redm[wave] = wm;
+                cbar(ctl, gen, a.err, failed);
+                const float M = fmaxf(fmaxf(sm.redm[0], sm.redm[1]), fmaxf(sm.redm[2], sm.redm[3]));
+                float lsum = 0.0f;
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
+                    const float e = valid ? expf(sc[i] - M) : 0.0f;
+                    lsum += e;
+                    acc.x = __builtin_fmaf(e, v4[i].x, acc.x);
+                    acc.y = __builtin_fmaf(e, v4[i].y, acc.y);
+                    acc.z = __builtin_fmaf(e, v4[i].z, acc.z);
+                    acc.w = __builtin_fmaf(e, v4[i].w, acc.w);
+                }
+                const float ws = wave_sum(sub == 0 ? lsum : 0.0f);
+                if (lane == 0) sm.reds[wave] = ws;
+                sm.accs[g][sub * 4 + 0] = acc.x;
+                sm.accs[g][sub * 4 + 1] = acc.y;
+                sm.accs[g][sub * 4 + 2] = acc.z;
+                sm.accs[g][sub * 4 + 3] = acc.w;
+                cbar(ctl, gen, a.err, failed);
+                if (act && tid < kHeadDim) {
+                    float tot = 0.0f;
+#pragma unroll
+                    for (int gg = 0; gg < 16; ++gg) tot += sm.accs[gg][tid];
+                    uint64_t* part = XW(sq) + kXpart + (static_cast<size_t>(h) * kAttnMaxSplits + s) * 68;
+                    xst(part + 4 + tid, epart, tot);
+                    if (tid == 0) {
+                        xst(part + 0, epart, M);
+                        xst(part + 1, epart, ((sm.reds[0] + sm.reds[1]) + sm.reds[2]) + sm.reds[3]);
+                    }
+                }
+                if (rd + 1 < P.rounds) cbar(ctl, gen, a.err, failed);
+            }
+            release_to(ctl, cb + P.o_proj, wave);
+            stores_done();
+        }
+
+        // ------------------------------------------------ merge of (sequence, head) = (b / 20, b % 20)
+        if (P.b < kHeads * B) {
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+            const int sq = P.b / kHeads, h = P.b % kHeads;
+            const int S = pick(P.S, sq);
+            const uint64_t* pb = XW(sq) + kXpart + static_cast<size_t>(h) * kAttnMaxSplits * 68;
+            if (S <= kMergeRegSplits) {
+                if (wave == 0) {
+                    constexpr int NR = kMergeRegSplits + 2;
+                    int idx[NR];
+                    bool use[NR];
+#pragma unroll
+                    for (int k = 0; k < kMergeRegSplits; ++k) {
+                        idx[k] = k * 68 + 4 + lane;
+                        use[k] = k < S;
+                    }
+                    idx[kMergeRegSplits] = lane * 68;
+                    idx[kMergeRegSplits + 1] = lane * 68 + 1;
+                    use[kMergeRegSplits] = use[kMergeRegSplits + 1] = lane < S;
+                    float v[NR];
+                    xread<NR>(pb, idx, use, ep(l, kEpPart), v, a.err, failed);
+                    const float mk = lane < S ? v[kMergeRegSplits] : -INFINITY;
+                    const float lk = lane < S ? v[kMergeRegSplits + 1] : 0.0f;
+                    const float mg = wave_max(mk);
+                    const float wk = mk == -INFINITY ? 0.0f : expf(mk - mg);
+                    float den[4] = {0.0f, 0.0f, 0.0f, 0.0f}, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int k = 0; k < kMergeRegSplits; ++k) {
+                        if (k < S) {
+                            const float wgt = lane_value(wk, k);
+                            den[k & 3] = __builtin_fmaf(lane_value(lk, k), wgt, den[k & 3]);
+                            num[k & 3] = __builtin_fmaf(v[k], wgt, num[k & 3]);
+                        }
+                    }
+                    const float d = ((den[0] + den[1]) + den[2]) + den[3];
+                    const float nn = ((num[0] + num[1]) + num[2]) + num[3];
+                    xst_bcast(XW(sq), kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
+                    stores_done();
+                }
+            } else {
+                constexpr int kRec = 2 + kHeadDim;
+                constexpr int NPT = (kAttnMaxSplits * kRec + kCT - 1) / kCT;
+                {
+                    int idx[NPT];
+                    bool use[NPT];
+                    float v[NPT];
+#pragma unroll
+                    for (int i = 0; i < NPT; ++i) {
+                        const int qq = tid + kCT * i;
+                        const int k = qq / kRec, f = qq % kRec;
+                        idx[i] = k * 68 + (f < 2 ? f : f + 2);
+                        use[i] = k < S;
+                    }
+                    xread<NPT>(pb, idx, use, ep(l, kEpPart), v, a.err, failed);
+#pragma unroll
+                    for (int i = 0; i < NPT; ++i) {
+                        const int qq = tid + kCT * i;
+                        if (use[i]) sm.mpart[qq / kRec][qq % kRec] = v[i];
+                    }
+                }
+                cbar(ctl, gen, a.err, failed);
+                if (wave == 0) {
+                    const float mk = lane < S ? sm.mpart[lane][0] : -INFINITY;
+                    const float lk = lane < S ? sm.mpart[lane][1] : 0.0f;
+                    const float mg = wave_max(mk);
+                    const float wk = mk == -INFINITY ? 0.0f : expf(mk - mg);
+                    float den[4] = {0.0f, 0.0f, 0.0f, 0.0f}, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int k0 = 0; k0 < S; k0 += 4) {
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) {
+                            const int k = k0 + w;
+                            if (k < S) {
+                                const float wgt = lane_value(wk, k);
+                                den[w] = __builtin_fmaf(lane_value(lk, k), wgt, den[w]);
+                                num[w] = __builtin_fmaf(sm.mpart[k][2 + lane], wgt, num[w]);
+                            }
+                        }
+                    }
+                    const float d = ((den[0] + den[1]) + den[2]) + den[3];
+                    const float nn = ((num[0] + num[1]) + num[2]) + num[3];
+                    xst_bcast(XW(sq), kXattn + h * kHeadDim + lane, ep(l, kEpAttn), nn / d);
+                    stores_done();
+                }
+                cbar(ctl, gen, a.err, failed);  // mpart aliases the staging area, written below
+            }
+        }
+
+        // ------------------------------------------------ attn.c_proj + residual
+        {
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+            const int cp = cb + P.o_proj;
+            int idx[5];
+            bool use[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                idx[i] = kXattn + tid + 256 * i;
+                use[i] = true;
+            }
+            XRead<5> xr[B];
+#pragma unroll
+            for (int q = 0; q < B; ++q) xr[q].issue(XR(q), idx, use, ep(l, kEpAttn));
+            LaneBias<kGProj, false> bias;
+            bias.load(par + kParProjB + P.p0, P.pn, wave, lane);
+#pragma unroll
+            for (int q = 0; q < B; ++q) {
+                float v[5];
+                xr[q].wait(XR(q), idx, ep(l, kEpAttn), v, a.err, failed);
+#pragma unroll
+                for (int i = 0; i < 5; ++i) sm.stage[q][tid + 256 * i] = v[i];
+            }
+            cbar(ctl, gen, a.err, failed);
+            const float* x[B];
+#pragma unroll
+            for (int q = 0; q < B; ++q) x[q] = sm.stage[q];
+            const uint32_t e = ep(l, kEpHmid);
+            auto out = [&](int k, float b, int q, float acc) { xst_bcast(XW(q), kXhmid + P.p0 + k, e, sm.resid_h[q][k] + (acc + b)); };
+            gemv_rows_b<B, RING, C::kFive>(ctl, ring, cp, P.pn, x, bias, par + kParProjB + P.p0, wave, lane, a.err, failed, out);
+            release_to(ctl, cb + P.o_fc, wave);
+            stores_done();
+            cbar(ctl, gen, a.err, failed);  // the staging area is written by the next phase
+        }
+
+        // ------------------------------------------------ LN2 + c_fc + GELU
+        {
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+            const int cf = cb + P.o_fc;
+            int idx[5];
+            bool use[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                idx[i] = kXhmid + tid + 256 * i;
+                use[i] = true;
+            }
+            XRead<5> xr[B];
+#pragma unroll
+            for (int q = 0; q < B; ++q) xr[q].issue(XR(q), idx, use, ep(l, kEpHmid));
+            LnPar ln;
+            ln.load(par + kParLn2W, par + kParLn2B, tid);
+            LaneBias<kGFc, false> bias;
+            bias.load(par + kParFcB + P.f0, P.fn, wave, lane);
+#pragma unroll
+            for (int q = 0; q < B; ++q) {
+                float hv[5];
+                xr[q].wait(XR(q), idx, ep(l, kEpHmid), hv, a.err, failed);
+#pragma unroll
+                for (int i = 0; i < 5; ++i) sm.stage[q][tid + 256 * i] = hv[i];
+            }
+            cbar(ctl, gen, a.err, failed);
+            if (wave == 0 && lane < P.gn) {
+#pragma unroll
+                for (int q = 0; q < B; ++q) sm.resid_m[q][lane] = sm.stage[q][P.g0 + lane];
+            }
+#pragma unroll
+            for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q], sm.stage[q] + kWidth, ln, tid, lane);
+            cbar(ctl, gen, a.err, failed);
+            const float* x[B];
+#pragma unroll
+            for (int q = 0; q < B; ++q) x[q] = sm.stage[q] + kWidth;
+            const uint32_t e = ep(l, kEpFf);
+            auto out = [&](int k, float b, int q, float acc) { xst_bcast(XW(q), kXff + P.f0 + k, e, gelu_f(acc + b)); };
+            gemv_rows_b<B, RING, C::kFive>(ctl, ring, cf, P.fn, x, bias, par + kParFcB + P.f0, wave, lane, a.err, failed, out);
+            release_to(ctl, cb + P.o_fc2, wave);
+            stores_done();
+            cbar(ctl, gen, a.err, failed);  // the staging area is written by the next phase
+        }
+
+        // ------------------------------------------------ mlp.c_proj + residual -> next h
+        {
+            const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+            const int cg = cb + P.o_fc2;
+            constexpr int NF = kFfn / kCT;
+            int idx[NF];
+            bool use[NF];
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                idx[i] = kXff + tid + kCT * i;
+                use[i] = true;
+            }
+            // At most 40 values per thread in flight (registers): B == 2 polls both sequences'
+            // 20 at once; larger batches poll every sequence's first 10, then every
+            // sequence's last 10 (two round trips instead of one per sequence).
+            constexpr int NH = B == 2 ? NF : NF / 2;
+#pragma unroll
+            for (int h0 = 0; h0 < NF; h0 += NH) {
+                int hidx[NH];
+                bool huse[NH];
+#pragma unroll
+                for (int i = 0; i < NH; ++i) {
+                    hidx[i] = idx[h0 + i];
+                    huse[i] = true;
+                }
+                XRead<NH> xr[B];
+#pragma unroll
+                for (int q = 0; q < B; ++q) xr[q].issue(XR(q), hidx, huse, ep(l, kEpFf));
+#pragma unroll
+                for (int q = 0; q < B; ++q) {
+                    float v[NH];
+                    xr[q].wait(XR(q), hidx, ep(l, kEpFf), v, a.err, failed);
+#pragma unroll
+                    for (int i = 0; i < NH; ++i) sm.stage[q][tid + kCT * (h0 + i)] = v[i];
+                }
+            }
+            cbar(ctl, gen, a.err, failed);
+            const int step_k = C::kPairs ? 8 : 4;
+            for (int k0 = wave; k0 < P.gn; k0 += step_k) {
+                float res[B];
+                rows_wide_b<B, RING, C::kPairs>(ctl, ring, cg, k0, P.gn, sm.stage, wave, lane, a.err, failed, res);
+                const int k = C::kPairs ? k0 + 4 * (lane >> 5) : k0;
+                const bool holder = C::kPairs ? (lane & 31) == 0 : lane == 0;
+                if (holder && k < P.gn) {
+                    const float b = par[kParFc2B + P.g0 + k];
+#pragma unroll
+                    for (int q = 0; q < B; ++q) xst_bcast(XW(q), kXh + P.g0 + k, ep(l + 1, kEpXh), sm.resid_m[q][k] + (res[q] + b));
+                }
+            }
+            release_to(ctl, (l + 1) * P.layer_chunks, wave);
+            stores_done();
+            cbar(ctl, gen, a.err, failed);  // the staging area is written by the next phase
+        }
+    }
+
+    // ---------------------------------------------------- ln_f, final_norm, mel_head
+    {
+        const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+        const int chd = a.layers * P.layer_chunks;
+        int idx[5];
+        bool use[5];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            idx[i] = kXh + tid + 256 * i;
+            use[i] = true;
+        }
+        XRead<5> xr[B];
+#pragma unroll
+        for (int q = 0; q < B; ++q) xr[q].issue(XR(q), idx, use, ep(a.layers, kEpXh));
+        LnPar lf;
+        lf.load(a.head + kHeadLnfW, a.head + kHeadLnfB, tid);
+        LnPar fn;
+        fn.load(a.head + kHeadFnW, a.head + kHeadFnB, tid);
+        LaneBias<kGHead, false> bias;
+        bias.load(a.head + kHeadBias + P.h0, P.hn, wave, lane);
+#pragma unroll
+        for (int q = 0; q < B; ++q) {
+            float hv[5];
+            xr[q].wait(XR(q), idx, ep(a.layers, kEpXh), hv, a.err, failed);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) sm.stage[q][tid + 256 * i] = hv[i];
+        }
+        cbar(ctl, gen, a.err, failed);
+        // ln_f, then final_norm, each into the next 1280 floats of the sequence's staging row
+#pragma unroll
+        for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q], sm.stage[q] + kWidth, lf, tid, lane);
+        cbar(ctl, gen, a.err, failed);
+#pragma unroll
+        for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q] + kWidth, sm.stage[q] + 2 * kWidth, fn, tid, lane);
+        cbar(ctl, gen, a.err, failed);
+        const float* x[B];
+#pragma unroll
+        for (int q = 0; q < B; ++q) x[q] = sm.stage[q] + 2 * kWidth;
+        auto out = [&](int k, float b, int q, float acc) { a.logits[static_cast<size_t>(q) * a.logit_stride + P.h0 + k] = acc + b; };
+        gemv_rows_b<B, RING, C::kFive>(ctl, ring, chd, P.hn, x, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
+        release_to(ctl, total_chunks, wave);
+    }
+}
+
+template <int B>
+hipError_t launch_b(const StepArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL(step_batch_kernel<B>, dim3(grid), dim3(kST), 0, s, a);
+    return hipGetLastError();
+}
+template <int B>
+hipError_t occupancy_b(int* blocks_per_cu) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, step_batch_kernel<B>, kST, 0);
+}
+
+}  // namespace
+
+// The merge of (sequence q, head h) runs on workgroup 20 q + h, and attn.c_proj / mlp.c_proj
+// give a workgroup at most kResidMax rows.
+bool step_batch_fits(int grid, int nseq) { return nseq >= 2 && nseq <= kStepBatchMax && grid >= kHeads * nseq && grid * kResidMax >= kWidth; }
+
+hipError_t step_batch_occupancy(int nseq, int* blocks_per_cu) {
+    switch (nseq) {
+        case 2: return occupancy_b<2>(blocks_per_cu);
+        case 3: return occupancy_b<3>(blocks_per_cu);
+        case 4: return occupancy_b<4>(blocks_per_cu);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_step_batch(const StepArgs& a, int nseq, int grid, hipStream_t s) {
+    if (nseq != a.nseq) return hipErrorInvalidValue;
+    switch (nseq) {
+        case 2: return launch_b<2>(a, grid, s);
+        case 3: return launch_b<3>(a, grid, s);
+        case 4: return launch_b<4>(a, grid, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace itts

@@ -335,6 +335,53 @@ def test_persistent_generate_equals_multikernel(both_paths, itts):
     assert step.cached_tokens() == multi.cached_tokens()
 
 
+@pytest.fixture(scope="module")
+def batch_paths(itts, small_weights):
+    """The 2-layer model with its stop token made likely (mel_head bias + 2.5), on the persistent
+    batch step (groups of up to 4 sequences per launch) and on the multi-kernel batch path."""
+    import os
+
+    w = dict(small_weights)
+    hb = w["gpt.mel_head.bias"].copy()
+    hb[8193] += 2.5
+    w["gpt.mel_head.bias"] = hb
+    old = os.environ.get("ITTS_GPT_PERSISTENT_BATCH")
+    try:
+        os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "0"
+        multi = itts.GptDecoder(w, kv_capacity=1024, max_batch=8)
+        os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "1"
+        step = itts.GptDecoder(w, kv_capacity=1024, max_batch=8)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT_BATCH"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT_BATCH"] = old
+    return step, multi
+
+
+@pytest.mark.parametrize("nseq", [2, 3, 4, 5, 7])
+def test_persistent_batch_generate_equals_multikernel(batch_paths, itts, nseq):
+    """Ragged prefixes (8..300 text ids: 1..6 attention splits per sequence), sampled codes, some
+    sequences stopping early (then inactive inside their launch group): the persistent batch
+    step and the multi-kernel path give the same codes, and each equals its batch-1 generate."""
+    step, multi = batch_paths
+    rng = np.random.default_rng(nseq)
+    prefixes, opts = [], []
+    for b in range(nseq):
+        cond, text = itts.synthetic_prefix_inputs(int(rng.integers(8, 300)), seed=200 + b)
+        prefixes.append(step.prepare_cond(cond, text, 0))
+        opts.append(itts.GenerationOptions(seed=300 + b, suppress_stop=b % 3 == 0))
+    print(f"persistent batch: nseq {nseq}", flush=True)
+    a = step.generate_batch(prefixes, opts, 40)
+    assert step.last_timing()["decode_path"] == "step"
+    b = multi.generate_batch(prefixes, opts, 40)
+    assert multi.last_timing()["decode_path"] == "multi"
+    assert [(r.codes, r.stopped) for r in a] == [(r.codes, r.stopped) for r in b]
+    for q in (0, nseq - 1):
+        single = step.generate(prefixes[q], opts[q], 40)
+        assert (single.codes, single.stopped) == (a[q].codes, a[q].stopped)
+
+
 @pytest.mark.gpu
 def test_decoder_from_bundle_bitwise_equals_arrays(itts, small_weights, tmp_path):
     """GptDecoder.from_bundle (zero-copy from the mapping) and GptDecoder(arrays) upload the

@@ -119,6 +119,7 @@ struct StepArgs {
     int nseq;
     size_t kv_slot_stride;
     int logit_stride;
+    const uint8_t* table;     // beam row-owner table [nseq][kv_cap] (slot holding each row) or null
 };
 bool step_fits(int grid);
 hipError_t step_occupancy(bool bf16, int* blocks_per_cu);

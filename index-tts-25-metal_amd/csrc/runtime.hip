@@ -152,6 +152,7 @@ struct Engine {
     // (bitwise the same logits as the multi-kernel path, which ITTS_GPT_PERSISTENT=0 selects).
     bool step_ok = false;
     bool step_batch_ok[kStepBatchMax + 1] = {};  // persistent batch step available for this many sequences
+    uint32_t beam_slots = 0;                     // slots the beam row-owner table may name (this search's beams)
     int step_grid = 0;
     int step_dev = 0;
     size_t per_layer = 0;       // weight elements per layer block
@@ -347,10 +348,11 @@ struct Engine {
         HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         HIP_CHECK(step_occupancy(false, &occ));
         if (occ < 1 || !step_fits(cus)) return;
-        // Batches of 2..4 sequences per launch (step_batch.hip), opt-in with
-        // ITTS_GPT_PERSISTENT_BATCH=1: it does not yet beat the multi-kernel path at batch > 1.
+        // Batches and beams of 2..4 sequences in one launch (step_batch.hip) when this decoder
+        // holds more than one sequence; ITTS_GPT_PERSISTENT_BATCH=0 keeps them on the
+        // multi-kernel path.
         const char* pb = std::getenv("ITTS_GPT_PERSISTENT_BATCH");
-        const bool batch = max_batch >= 2 && pb && std::strcmp(pb, "1") == 0;
+        const bool batch = max_batch >= 2 && !(pb && std::strcmp(pb, "0") == 0);
         for (int nb = 2; batch && nb <= kStepBatchMax; ++nb) {
             int bocc = 0;
             HIP_CHECK(step_batch_occupancy(nb, &bocc));
@@ -410,19 +412,19 @@ struct Engine {
             throw std::runtime_error("GPT decode step: a workgroup hand-off timed out");
         }
     }
-    // The persistent path covers nseq sequences in launches of up to kStepBatchMax (the last
-    // launch takes the remainder; one sequence goes to the batch-1 step).
+    // The persistent path takes one sequence (step.hip) or 2..kStepBatchMax in one launch
+    // (step_batch.hip; with the beam row-owner table when every slot it may name is below
+    // kStepBatchMax).  Larger batches stay on the multi-kernel path, whose batched GEMVs read
+    // the weights once for all of them (measured faster from 5 sequences on).
     bool persistent(int nseq, bool use_table) const {
-        if (!step_ok || use_table || nseq < 1) return false;
-        if (nseq == 1) return true;
-        const int rem = nseq % kStepBatchMax;
-        return (nseq < kStepBatchMax || step_batch_ok[kStepBatchMax]) && (rem < 2 || step_batch_ok[rem]);
+        if (!step_ok || nseq < 1 || nseq > kStepBatchMax) return false;
+        if (use_table) return nseq >= 2 && step_batch_ok[nseq] && beam_slots <= static_cast<uint32_t>(kStepBatchMax);
+        return nseq == 1 || step_batch_ok[nseq];
     }
-    void launch_persistent(int nseq) {
-        for (int q0 = 0; q0 < nseq; q0 += kStepBatchMax) {
-            const int nq = std::min(kStepBatchMax, nseq - q0);
-            HIP_CHECK(launch_step_serialized(step_args(q0, nq), nq, step_grid, bf16, step_dev, stream));
-        }
+    void launch_persistent(int nseq, bool use_table) {
+        StepArgs s = step_args(0, nseq);
+        s.table = use_table ? table.p : nullptr;
+        HIP_CHECK(launch_step_serialized(s, nseq, step_grid, bf16, step_dev, stream));
     }
 
     // ---------------------------------------------------------------- forward pieces
@@ -542,7 +544,7 @@ struct Engine {
     void run_step(int nseq, int nb, bool sampler, bool use_table) {
         if (persistent(nseq, use_table)) {
             timing.decode_path = ITTS_PATH_STEP;
-            launch_persistent(nseq);
+            launch_persistent(nseq, use_table);
             if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
             return;
         }
@@ -1007,7 +1009,7 @@ struct Engine {
                     enqueue_head(batch, nb);
                     break;
                 case 6:
-                    launch_persistent(batch);
+                    launch_persistent(batch, false);
                     break;
                 default: {
                     AttnArgs t{};
@@ -1102,6 +1104,7 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
     };
     std::vector<Finished> finished;
     const uint32_t take = 2 * nbeam;
+    beam_slots = nbeam;
     beam_scores.ensure(kMaxBatch);
     all_scores.ensure(static_cast<size_t>(kMaxBatch) * kMelVocab);
     beam_list.ensure(static_cast<size_t>(kMaxBatch) * kMelVocab);

@@ -5,10 +5,10 @@
 // What is per sequence q:
 //   * the exchange: sequence q owns a whole batch-1 exchange layout at q * kStepExchangeTotal
 //     (broadcast copies included), tagged with the launch's epochs;
-//   * the KV cache of slot q (kv + q * kv_slot_stride), its cached length n_q and its
-//     attention tiles: the tile list is sequence 0's 20 x S_0 tiles, then sequence 1's, ...,
-//     dealt to workgroups round by round as in step.hip; the merge of (q, head h) runs on
-//     workgroup 20 q + h;
+//   * the KV cache of slot q (kv + q * kv_slot_stride; with a beam row-owner table, row r of
+//     sequence q is in slot table[q][r]), its cached length n_q and its attention tiles: the
+//     tile list is sequence 0's 20 x S_0 tiles, then sequence 1's, ..., dealt to workgroups
+//     round by round as in step.hip; the merge of (q, head h) runs on workgroup 20 q + h;
 //   * the logits row (logits + q * logit_stride) and the decode state (state[q]).
 // A workgroup's GEMV rows are the same as in step.hip; each row group's weights are read
 // from the LDS ring once and multiplied with the B input vectors (B FMA chains, each in the
@@ -23,6 +23,13 @@
 // registers hold only the row group's weights and B accumulators.  Since consecutive phases
 // reuse the staging area, each phase ends its reads of it at a compute-wave barrier before
 // the next phase writes.
+//
+// Attention differs from step.hip in where the cached K/V rows come from: the compute threads
+// load their tile rows straight into registers, two rounds ahead, instead of the loaders
+// staging them in the ring.  Those rows are in the cache before the step starts, so their
+// loads overlap the q hand-off, and with several rounds per layer no round waits behind
+// the loaders' weight stream.  q and the new K/V row of a window of four rounds are polled
+// once into LDS.  The loaders stream weights only.
 //
 // Reference ops replaced: gpt.cpp:88-125 for several step rows (as step.hip), the batched
 // form of the reference's per-row GEMV (kernels.metal mit2_linear_gemv_f32 :1054-1080).
@@ -67,7 +74,7 @@ struct PlanB {
     int active[B];                                   // per sequence: still decoding (its K/V row is appended)
     int ntiles, rounds;
     int q0, qn, p0, pn, f0, fn, g0, gn, h0, hn;  // row slices: c_attn, c_proj, c_fc, mlp.c_proj, mel_head
-    int att_chunks, layer_chunks;
+    int layer_chunks;
     int o_att, o_proj, o_fc, o_fc2;
 
     __device__ static void slice(int rows, int G, int b, int& r0, int& cnt) {
@@ -94,7 +101,6 @@ struct PlanB {
         R = max(0, min(t1, pick(n, sq)) - t0);
         return true;
     }
-    __device__ __forceinline__ static int kv_chunks(int R) { return (R + kKvRowsPerChunk - 1) / kKvRowsPerChunk; }
 
     __device__ __forceinline__ void init(const SeqState* st, int splits) {
         G = static_cast<int>(gridDim.x);
@@ -116,13 +122,8 @@ struct PlanB {
         slice(kFfn, G, b, f0, fn);
         slice(kWidth, G, b, g0, gn);
         slice(kMelVocab, G, b, h0, hn);
-        att_chunks = 0;
-        for (int rd = 0; rd < rounds; ++rd) {
-            int sq, h, s, t0, R;
-            if (tile(rd, sq, h, s, t0, R)) att_chunks += 2 * kv_chunks(R);
-        }
         o_att = qn;
-        o_proj = o_att + att_chunks;
+        o_proj = o_att;  // cached K/V rows are loaded by the compute threads, not streamed
         o_fc = o_proj + pn;
         o_fc2 = o_fc + fn;
         layer_chunks = o_fc2 + 4 * gn;
@@ -143,8 +144,7 @@ struct SmemB {
 
 // ------------------------------------------------------------------ loader waves
 
-// chunk_src of step.hip with the tiles of several sequences: a K/V chunk reads sequence sq's
-// cache slot.
+// chunk_src of step.hip without the K/V chunks (the compute threads load those).
 template <int B>
 __device__ __forceinline__ void chunk_src_b(const StepArgs& a, const PlanB<B>& P, const float* W, int l, int r, int lane,
                                             const float*& base, uint32_t& extent, uint32_t (&off)[kLines]) {
@@ -154,27 +154,6 @@ __device__ __forceinline__ void chunk_src_b(const StepArgs& a, const PlanB<B>& P
         const float* wl = W + static_cast<size_t>(l) * a.layer_stride;
         if (r < P.o_att) {
             base = wl + static_cast<size_t>(P.q0 + r) * kWidth;
-        } else if (r < P.o_proj) {
-            int q = r - P.o_att, sq = 0, h = 0, s = 0, t0 = 0, R = 0, kc = 0;
-            for (int rd = 0; rd < P.rounds; ++rd) {
-                if (!P.tile(rd, sq, h, s, t0, R)) continue;
-                kc = PlanB<B>::kv_chunks(R);
-                if (q < 2 * kc) break;
-                q -= 2 * kc;
-            }
-            const bool is_v = q >= kc;
-            const int j = is_v ? q - kc : q;
-            const float* kvb = a.kv + static_cast<size_t>(sq) * a.kv_slot_stride + static_cast<size_t>(l) * a.kv_layer_stride +
-                               (is_v ? a.kv_v_off : 0) + static_cast<size_t>(h) * a.kv_cap * kHeadDim;
-            base = kvb + static_cast<size_t>(t0) * kHeadDim;
-            extent = static_cast<uint32_t>(R) * kHeadDim * 4;
-#pragma unroll
-            for (int k = 0; k < kLines; ++k) {
-                int row = kKvRowsPerChunk * j + 4 * k + (lane >> 4);  // tile-local row
-                if (row >= R) row = 0;                                 // clamped: loaded, never read
-                off[k] = static_cast<uint32_t>((row * kHeadDim + (lane & 15) * 4) * 4);
-            }
-            return;
         } else if (r < P.o_fc) {
             base = wl + static_cast<size_t>(kQkv) * kWidth + static_cast<size_t>(P.p0 + r - P.o_proj) * kWidth;
         } else if (r < P.o_fc2) {
@@ -192,14 +171,54 @@ __device__ __forceinline__ void chunk_src_b(const StepArgs& a, const PlanB<B>& P
 
 // ------------------------------------------------------------------ compute waves
 
-// dst = LayerNorm(row) for this thread's 5 columns (tid + 256 i); the statistics are those of
-// ln_stats (every wave forms them for the whole row), so the values equal ln_to_xrow's.
-__device__ __forceinline__ void ln_rows_to(const float* row, float* dst, const LnPar& p, int tid, int lane) {
-    float v[4][5], mean, inv;
-    ln_layout_load(row, lane, v);
-    ln_stats(v, mean, inv);
+// Element offsets (from a.kv) of the cached K rows of round rd's tile that thread (g, sub)
+// holds: rows g + 16 i (i < 4), columns 4 sub .. 4 sub + 3; ~0u for rows at or past the
+// tile's cached rows.  The V rows sit a.kv_v_off further.  (The offsets fit 32 bits:
+// launch_step_batch checks kStepBatchMax * kv_slot_stride.)
+template <int B>
+__device__ __forceinline__ void tile_rows(const StepArgs& a, const PlanB<B>& P, int rd, size_t kvl, int g, int sub, uint32_t (&off)[4]) {
+    int sq = 0, h = 0, s = 0, t0 = 0, R = 0;
+    const bool act = P.tile(rd, sq, h, s, t0, R);
 #pragma unroll
-    for (int i = 0; i < 5; ++i) dst[tid + 256 * i] = ln_apply(row[tid + 256 * i], mean, inv, p.g[i], p.b[i]);
+    for (int i = 0; i < 4; ++i) {
+        const int r = g + 16 * i;
+        off[i] = ~0u;
+        if (act && r < R) {
+            const int row = t0 + r;
+            const int slot = a.table ? static_cast<int>(a.table[static_cast<size_t>(sq) * a.kv_cap + row]) : sq;
+            off[i] = static_cast<uint32_t>(static_cast<size_t>(slot) * a.kv_slot_stride + kvl +
+                                           (static_cast<size_t>(h) * a.kv_cap + row) * kHeadDim + sub * 4);
+        }
+    }
+}
+// Issues the loads of four rows (zero where off is ~0u); the compiler waits for them where
+// they are used.
+__device__ __forceinline__ void load_rows(const float* base, const uint32_t (&off)[4], float4 (&d)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = off[i] != ~0u ? *reinterpret_cast<const float4*>(base + off[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+constexpr int kQWin = 4;    // rounds whose q / new K / new V are polled together
+constexpr int kQRec = 192;  // floats per round in the window: q, new K, new V (64 each)
+
+// dst[q] = LayerNorm(row[q]) for this thread's 5 columns (tid + 256 i) of each of B rows; the
+// statistics are those of ln_stats (every wave forms them for the whole row), so the values
+// equal ln_to_xrow's.  All rows are read before any is written, so the B reductions run
+// interleaved (row by row, each output store would have to precede the next row's loads).
+template <int B>
+__device__ __forceinline__ void ln_rows_to(const float* const (&row)[B], float* const (&dst)[B], const LnPar& p, int tid, int lane) {
+    float v[B][4][5], mean[B], inv[B], own[B][5];
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+        ln_layout_load(row[q], lane, v[q]);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) own[q][i] = row[q][tid + 256 * i];
+    }
+#pragma unroll
+    for (int q = 0; q < B; ++q) ln_stats(v[q], mean[q], inv[q]);
+#pragma unroll
+    for (int q = 0; q < B; ++q)
+#pragma unroll
+        for (int i = 0; i < 5; ++i) dst[q][tid + 256 * i] = ln_apply(own[q][i], mean[q], inv[q], p.g[i], p.b[i]);
 }
 
 // rowsN of step.hip for B inputs: rows k0 + 4 t (t < N, those below cnt) of a 1280-wide slice,
@@ -417,8 +436,16 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
 #pragma unroll
                 for (int q = 0; q < B; ++q) sm.resid_h[q][lane] = sm.stage[q][P.p0 + lane];
             }
+            {
+                const float* rows[B];
+                float* dst[B];
 #pragma unroll
-            for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q], sm.stage[q] + kWidth, ln, tid, lane);
+                for (int q = 0; q < B; ++q) {
+                    rows[q] = sm.stage[q];
+                    dst[q] = sm.stage[q] + kWidth;
+                }
+                ln_rows_to<B>(rows, dst, ln, tid, lane);
+            }
             cbar(ctl, gen, a.err, failed);
             const float* x[B];
 #pragma unroll
@@ -446,78 +473,79 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
             const int g = tid >> 4, sub = tid & 15;
             const uint32_t eq = ep(l, kEpQkv), epart = ep(l, kEpPart);
-            int ca = cb + P.o_att;
-            release_to(ctl, ca, wave);
+            release_to(ctl, cb + P.o_att, wave);  // c_attn's rows are done: the loaders go on to c_proj
+            // The window of q / new K / new V records sits in the staging area past the two
+            // 1280-float rows (raw and normalised h) that c_attn reads, so it may be written
+            // while other waves still run c_attn.
+            float* qwin = &sm.stage[0][2 * kWidth];
+            // One tile's rows in registers: the next round's K is issued once this round's
+            // scores are formed, its V once this round's weighted sum is.
+            uint32_t off[4];
+            float4 kk[4], vv[4];
+            tile_rows<B>(a, P, 0, kvl, g, sub, off);
+            load_rows(a.kv, off, kk);
+            load_rows(a.kv + a.kv_v_off, off, vv);
             for (int rd = 0; rd < P.rounds; ++rd) {
+                // A later window overwrites the last one after the previous round's closing
+                // barrier; every wave read its record before that round's first barrier.
+                if (rd % kQWin == 0) {
+                    if (tid < kQRec) {
+                        const int part = tid >> 6, c = tid & 63;  // part 0: q, 1: new K, 2: new V
+                        int idx[kQWin];
+                        bool use[kQWin];
+#pragma unroll
+                        for (int w = 0; w < kQWin; ++w) {
+                            int sq = 0, h = 0, s = 0, t0 = 0, R = 0;
+                            const bool act = P.tile(rd + w, sq, h, s, t0, R);
+                            const int nq = act ? pick(P.n, sq) : 0;
+                            const int p1 = act ? min(pick(P.L, sq), t0 + pick(P.chunk_rows, sq)) : 0;
+                            idx[w] = sq * static_cast<int>(kStepExchangeTotal) + kXqkv + part * kWidth + h * kHeadDim + c;
+                            use[w] = act && (part == 0 || (nq >= t0 && nq < p1));
+                        }
+                        float v[kQWin];
+                        xread<kQWin>(XR(0), idx, use, eq, v, a.err, failed);
+#pragma unroll
+                        for (int w = 0; w < kQWin; ++w)
+                            if (use[w]) qwin[w * kQRec + tid] = v[w];
+                    }
+                    cbar(ctl, gen, a.err, failed);
+                }
                 int sq = 0, h = 0, s = 0, t0 = 0, R = 0;
                 const bool act = P.tile(rd, sq, h, s, t0, R);
                 const int nq = act ? pick(P.n, sq) : 0;
                 const int p1 = act ? min(pick(P.L, sq), t0 + pick(P.chunk_rows, sq)) : 0;
-                const int kc = act ? PlanB<B>::kv_chunks(R) : 0;
-                constexpr int PER = kAttnMaxChunk / 16;
-                constexpr int PERL = 4;
-                float4 k4[PER], v4[PER];
-#pragma unroll
-                for (int i = 0; i < PER; ++i) {
-                    k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    v4[i] = k4[i];
-                }
                 const int dn = nq - t0 - g;
-                const int i_new = (act && nq < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < PERL) ? (dn >> 4) : -1;
-                int idx[12];
-                bool use[12];
+                const int i_new = (act && nq < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < 4) ? (dn >> 4) : -1;
+                const float* qr = qwin + (rd % kQWin) * kQRec;
+                const float4 q4 = *reinterpret_cast<const float4*>(qr + sub * 4);
+                if (i_new >= 0) {
+                    const float4 kn = *reinterpret_cast<const float4*>(qr + kHeadDim + sub * 4);
+                    const float4 vn = *reinterpret_cast<const float4*>(qr + 2 * kHeadDim + sub * 4);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    idx[k] = kXqkv + h * kHeadDim + sub * 4 + k;
-                    idx[4 + k] = kXqkv + kWidth + h * kHeadDim + sub * 4 + k;
-                    idx[8 + k] = kXqkv + 2 * kWidth + h * kHeadDim + sub * 4 + k;
-                    use[k] = act;
-                    use[4 + k] = use[8 + k] = i_new >= 0;
-                }
-                const uint64_t* XQ = XR(act ? sq : 0);
-                XRead<12> xr;
-                xr.issue(XQ, idx, use, eq);
-                for (int j = 0; j < 2 * kc; ++j) (void)wait_chunk<RING>(ctl, ring, ca + j, a.err, failed);
-#pragma unroll
-                for (int i = 0; i < PERL; ++i) {
-                    const int r = g + 16 * i;
-                    if (act && r < R) {
-                        const float* kch = ring + ((ca + r / kKvRowsPerChunk) % RING) * kChunkF;
-                        const float* vch = ring + ((ca + kc + r / kKvRowsPerChunk) % RING) * kChunkF;
-                        const int off = (r % kKvRowsPerChunk) * kHeadDim + sub * 4;
-                        k4[i] = *reinterpret_cast<const float4*>(kch + off);
-                        v4[i] = *reinterpret_cast<const float4*>(vch + off);
-                    }
-                }
-                ca += 2 * kc;
-                release_to(ctl, ca, wave);
-                float4 q4;
-                {
-                    float qv[12];
-                    xr.wait(XQ, idx, eq, qv, a.err, failed);
-                    q4 = make_float4(qv[0], qv[1], qv[2], qv[3]);
-                    const float4 kn = make_float4(qv[4], qv[5], qv[6], qv[7]);
-                    const float4 vn = make_float4(qv[8], qv[9], qv[10], qv[11]);
-#pragma unroll
-                    for (int i = 0; i < PER; ++i) {
+                    for (int i = 0; i < 4; ++i) {
                         if (i == i_new) {
-                            k4[i] = kn;
-                            v4[i] = vn;
+                            kk[i] = kn;
+                            vv[i] = vn;
                         }
                     }
                 }
-                float sc[PER];
+                float sc[4];
                 float mloc = -INFINITY;
 #pragma unroll
-                for (int i = 0; i < PER; ++i) {
-                    float d = q4.x * k4[i].x;
-                    d = __builtin_fmaf(q4.y, k4[i].y, d);
-                    d = __builtin_fmaf(q4.z, k4[i].z, d);
-                    d = __builtin_fmaf(q4.w, k4[i].w, d);
+                for (int i = 0; i < 4; ++i) {
+                    float d = q4.x * kk[i].x;
+                    d = __builtin_fmaf(q4.y, kk[i].y, d);
+                    d = __builtin_fmaf(q4.z, kk[i].z, d);
+                    d = __builtin_fmaf(q4.w, kk[i].w, d);
                     d = sum16_up(d);
-                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
+                    const bool valid = act && t0 + g + 16 * i < p1;
                     sc[i] = valid ? d * 0.125f : -INFINITY;
                     mloc = fmaxf(mloc, sc[i]);
+                }
+                const bool more = rd + 1 < P.rounds;
+                if (more) {
+                    tile_rows<B>(a, P, rd + 1, kvl, g, sub, off);
+                    load_rows(a.kv, off, kk);
                 }
                 const float wm = wave_max(mloc);
                 if (lane == 0) sm.redm[wave] = wm;
@@ -526,15 +554,16 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
                 float lsum = 0.0f;
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                for (int i = 0; i < PER; ++i) {
-                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
+                for (int i = 0; i < 4; ++i) {
+                    const bool valid = act && t0 + g + 16 * i < p1;
                     const float e = valid ? expf(sc[i] - M) : 0.0f;
                     lsum += e;
-                    acc.x = __builtin_fmaf(e, v4[i].x, acc.x);
-                    acc.y = __builtin_fmaf(e, v4[i].y, acc.y);
-                    acc.z = __builtin_fmaf(e, v4[i].z, acc.z);
-                    acc.w = __builtin_fmaf(e, v4[i].w, acc.w);
+                    acc.x = __builtin_fmaf(e, vv[i].x, acc.x);
+                    acc.y = __builtin_fmaf(e, vv[i].y, acc.y);
+                    acc.z = __builtin_fmaf(e, vv[i].z, acc.z);
+                    acc.w = __builtin_fmaf(e, vv[i].w, acc.w);
                 }
+                if (more) load_rows(a.kv + a.kv_v_off, off, vv);
                 const float ws = wave_sum(sub == 0 ? lsum : 0.0f);
                 if (lane == 0) sm.reds[wave] = ws;
                 sm.accs[g][sub * 4 + 0] = acc.x;
@@ -553,7 +582,7 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
                         xst(part + 1, epart, ((sm.reds[0] + sm.reds[1]) + sm.reds[2]) + sm.reds[3]);
                     }
                 }
-                if (rd + 1 < P.rounds) cbar(ctl, gen, a.err, failed);
+                if (more) cbar(ctl, gen, a.err, failed);
             }
             release_to(ctl, cb + P.o_proj, wave);
             stores_done();
@@ -711,8 +740,16 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
 #pragma unroll
                 for (int q = 0; q < B; ++q) sm.resid_m[q][lane] = sm.stage[q][P.g0 + lane];
             }
+            {
+                const float* rows[B];
+                float* dst[B];
 #pragma unroll
-            for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q], sm.stage[q] + kWidth, ln, tid, lane);
+                for (int q = 0; q < B; ++q) {
+                    rows[q] = sm.stage[q];
+                    dst[q] = sm.stage[q] + kWidth;
+                }
+                ln_rows_to<B>(rows, dst, ln, tid, lane);
+            }
             cbar(ctl, gen, a.err, failed);
             const float* x[B];
 #pragma unroll
@@ -809,11 +846,27 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
         }
         cbar(ctl, gen, a.err, failed);
         // ln_f, then final_norm, each into the next 1280 floats of the sequence's staging row
+        {
+            const float* rows[B];
+            float* dst[B];
 #pragma unroll
-        for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q], sm.stage[q] + kWidth, lf, tid, lane);
+            for (int q = 0; q < B; ++q) {
+                rows[q] = sm.stage[q];
+                dst[q] = sm.stage[q] + kWidth;
+            }
+            ln_rows_to<B>(rows, dst, lf, tid, lane);
+        }
         cbar(ctl, gen, a.err, failed);
+        {
+            const float* rows[B];
+            float* dst[B];
 #pragma unroll
-        for (int q = 0; q < B; ++q) ln_rows_to(sm.stage[q] + kWidth, sm.stage[q] + 2 * kWidth, fn, tid, lane);
+            for (int q = 0; q < B; ++q) {
+                rows[q] = sm.stage[q] + kWidth;
+                dst[q] = sm.stage[q] + 2 * kWidth;
+            }
+            ln_rows_to<B>(rows, dst, fn, tid, lane);
+        }
         cbar(ctl, gen, a.err, failed);
         const float* x[B];
 #pragma unroll
@@ -850,7 +903,9 @@ hipError_t step_batch_occupancy(int nseq, int* blocks_per_cu) {
 }
 
 hipError_t launch_step_batch(const StepArgs& a, int nseq, int grid, hipStream_t s) {
-    if (nseq != a.nseq) return hipErrorInvalidValue;
+    // tile_rows forms 32-bit element offsets into slots 0 .. kStepBatchMax - 1 (of the launch's
+    // KV base): the sequences' own, or those the row-owner table names
+    if (nseq != a.nseq || static_cast<uint64_t>(kStepBatchMax) * a.kv_slot_stride >= 0xFFFFFFFFull) return hipErrorInvalidValue;
     switch (nseq) {
         case 2: return launch_b<2>(a, grid, s);
         case 3: return launch_b<3>(a, grid, s);

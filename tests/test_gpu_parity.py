@@ -362,8 +362,9 @@ def batch_paths(itts, small_weights):
 @pytest.mark.parametrize("nseq", [2, 3, 4, 5, 7])
 def test_persistent_batch_generate_equals_multikernel(batch_paths, itts, nseq):
     """Ragged prefixes (8..300 text ids: 1..6 attention splits per sequence), sampled codes, some
-    sequences stopping early (then inactive inside their launch group): the persistent batch
-    step and the multi-kernel path give the same codes, and each equals its batch-1 generate."""
+    sequences stopping early (then inactive inside the launch): the persistent batch step (up to
+    4 sequences; more stay on the multi-kernel path) and the multi-kernel path give the same
+    codes, and each equals its batch-1 generate."""
     step, multi = batch_paths
     rng = np.random.default_rng(nseq)
     prefixes, opts = [], []
@@ -373,13 +374,37 @@ def test_persistent_batch_generate_equals_multikernel(batch_paths, itts, nseq):
         opts.append(itts.GenerationOptions(seed=300 + b, suppress_stop=b % 3 == 0))
     print(f"persistent batch: nseq {nseq}", flush=True)
     a = step.generate_batch(prefixes, opts, 40)
-    assert step.last_timing()["decode_path"] == "step"
+    assert step.last_timing()["decode_path"] == ("step" if nseq <= 4 else "multi")
     b = multi.generate_batch(prefixes, opts, 40)
     assert multi.last_timing()["decode_path"] == "multi"
     assert [(r.codes, r.stopped) for r in a] == [(r.codes, r.stopped) for r in b]
     for q in (0, nseq - 1):
         single = step.generate(prefixes[q], opts[q], 40)
         assert (single.codes, single.stopped) == (a[q].codes, a[q].stopped)
+
+
+@pytest.mark.parametrize("opts", [
+    dict(do_sample=False, num_beams=3, repetition_penalty=10.0, suppress_stop=True),
+    dict(do_sample=False, num_beams=4, length_penalty=1.0),
+    dict(do_sample=True, seed=5, num_beams=3),
+    dict(do_sample=True, seed=6, num_beams=2, top_k=0, top_p=0.9, temperature=1.2),
+])
+def test_persistent_beam_search_equals_multikernel(batch_paths, itts, opts):
+    """Beam search on the persistent batch step, children reading their parents' cached rows
+    through the row-owner table, gives the multi-kernel path's codes (the stop bias ends
+    beams, so the number of children per step varies)."""
+    step, multi = batch_paths
+    cond, text = itts.synthetic_prefix_inputs(50, seed=9)
+    prefix = step.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(**opts)
+    print(f"persistent beams: {opts}", flush=True)
+    a = step.generate(prefix, o, 32)
+    if o.suppress_stop:
+        assert step.last_timing()["decode_path"] == "step"
+    b = multi.generate(prefix, o, 32)
+    assert multi.last_timing()["decode_path"] == "multi"
+    assert (a.codes, a.stopped) == (b.codes, b.stopped)
+    assert step.cached_tokens() == multi.cached_tokens()
 
 
 @pytest.mark.gpu

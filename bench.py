@@ -21,6 +21,7 @@ weights.
     python bench.py --kernel-only gemv_c_fc --iters 240   # one kernel kind, for profilers
 """
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -83,7 +84,7 @@ def timed(fn, reps: int):
 
 
 def extras(it, dec, weights):
-    """Beam-3, long-context and batch-8 (FP32, BF16) workloads of the same model."""
+    """Beam-3, long-context, 8-segment request and batch-8 (FP32, BF16) workloads of the same model."""
     res = {}
     # Beam search, 3 beams: 32 latents + 80 text ids, 400 codes, length penalty 0, repetition penalty 10.
     cond, text = it.synthetic_prefix_inputs(80, seed=3)
@@ -121,6 +122,23 @@ def extras(it, dec, weights):
         cond, text = it.synthetic_prefix_inputs(int(rng.integers(24, 201)), seed=100 + b)
         prefixes.append(dec.prepare_cond(cond, text, 0))
         opts.append(it.GenerationOptions(seed=1000 + b, suppress_stop=True))
+    # One request's text segments (NativeRuntime's loop, native_runtime.cpp:98-99): 8 segments
+    # of U[24, 120] text ids (seed 11), speaker/emotion conditioning, 300 sampled codes each.
+    # generate_segments decodes them together; the reference's loop runs them one at a time.
+    rng = np.random.default_rng(11)
+    segs = [[int(x) for x in rng.integers(0, 12000, int(rng.integers(24, 121)))] for _ in range(8)]
+    sp, em = it.synthetic_normal(192, 5), it.synthetic_normal(1280, 6)
+    so = it.GenerationOptions(seed=500, suppress_stop=True)
+    dec.generate_segments(sp, em, segs, 0, so, 16)
+    r, times = timed(lambda: dec.generate_segments(sp, em, segs, 0, so, 300), 2)
+    loop, ltimes = timed(lambda: [dec.generate(dec.prepare(sp, em, s, 0), dataclasses.replace(so, seed=so.seed + i), 300)
+                                  for i, s in enumerate(segs)], 1)
+    total = sum(len(x.codes) for x in r)
+    res["segments8_f32"] = {
+        "codes": total, "seconds": round(min(times), 4), "tokens_per_s": round(total / min(times), 2),
+        "loop_seconds": round(min(ltimes), 4), "loop_tokens_per_s": round(total / min(ltimes), 2),
+        "same_codes_as_loop": [x.codes for x in r] == [x.codes for x in loop],
+    }
     for dtype in ("f32", "bf16"):
         d = dec if dtype == "f32" else it.GptDecoder(weights, kv_capacity=4096, max_batch=8, weight_dtype="bf16")
         d.generate_batch(prefixes, opts, 16)

@@ -156,6 +156,27 @@ int itts_gpt_generate_batch(itts_gpt* h, uint32_t batch, const float* const* pre
                             const itts_gen_options* options, uint32_t max_tokens, uint32_t* codes_out,
                             uint32_t* n_codes, int32_t* stopped);
 
+/* The GPT part of NativeRuntime::synthesize's segment loop (src/native_runtime.cpp:98-99),
+ * for all of one request's text segments at once.  For segment i:
+ *   prefix_i = prepare(speaker, emotion, ids_i, language)   (gpt.cpp:42-71)
+ *   result_i = generate(prefix_i, options with seed + i, max_tokens)
+ * where ids_i is the next id_counts[i] entries of ids (segments back to back).  Every
+ * segment is checked in order, with prepare's and generate's messages, before any work
+ * starts.  The prefixes are built on the device, and the segments are decoded together
+ * up to max_batch at a time.  With num_beams > 1 they are decoded one at a time.  The
+ * codes equal those of the sequential loop.  codes_out is [n_segments][max_tokens].
+ * Afterwards cached_tokens() is that of the first segment of the last decoded group. */
+int itts_gpt_generate_segments(itts_gpt* h, const float* speaker, const float* emotion, const uint32_t* ids,
+                               const uint32_t* id_counts, uint32_t n_segments, uint32_t language,
+                               const itts_gen_options* options, uint32_t max_tokens, uint32_t* codes_out,
+                               uint32_t* n_codes, int32_t* stopped);
+/* Same, with caller-given conditioning rows (n_cond x 1280) in place of the
+ * [spk_proj(speaker) + emotion, 0, 0] block, as itts_gpt_prepare_cond. */
+int itts_gpt_generate_segments_cond(itts_gpt* h, const float* cond, uint32_t n_cond, const uint32_t* ids,
+                                    const uint32_t* id_counts, uint32_t n_segments, uint32_t language,
+                                    const itts_gen_options* options, uint32_t max_tokens, uint32_t* codes_out,
+                                    uint32_t* n_codes, int32_t* stopped);
+
 /* apply_gpt_sampling_processors (gpt_sampling.cpp:28-128), run on the device. */
 int itts_gpt_apply_processors(itts_gpt* h, const float* logits, uint32_t vocab, const uint32_t* history,
                               uint32_t n_history, const itts_gen_options* options, float* out);

@@ -3,6 +3,7 @@
 // src/gpt_sampling.cpp:168-245; the math runs in libitts_gpt.so on the MI355X.
 #include "itts25/gpt.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <stdexcept>
@@ -181,6 +182,29 @@ GenerationResult GptDecoder::generate(const std::vector<float>& prefix, const Ge
                             &stopped));
     codes.resize(n);
     return {std::move(codes), stopped != 0};
+}
+
+std::vector<GenerationResult> GptDecoder::generate_segments(const std::vector<float>& speaker, const std::vector<float>& emotion,
+                                                            const std::vector<std::vector<uint32_t>>& segments, uint32_t language,
+                                                            const GenerationOptions& options, uint32_t max_tokens) {
+    if (speaker.size() != 192 || emotion.size() != 1280) throw std::invalid_argument("Invalid GPT conditioning dimensions");
+    std::vector<uint32_t> ids, counts;
+    for (const auto& seg : segments) {
+        ids.insert(ids.end(), seg.begin(), seg.end());
+        counts.push_back(static_cast<uint32_t>(seg.size()));
+    }
+    const itts_gen_options c = to_c(options);
+    const size_t n = segments.size(), stride = max_tokens ? max_tokens : 1;
+    std::vector<uint32_t> codes(std::max<size_t>(n, 1) * stride), lengths(std::max<size_t>(n, 1));
+    std::vector<int32_t> stopped(std::max<size_t>(n, 1));
+    check(itts_gpt_generate_segments(handle_, speaker.data(), emotion.data(), ids.data(), counts.data(), static_cast<uint32_t>(n),
+                                     language, &c, max_tokens, codes.data(), lengths.data(), stopped.data()));
+    std::vector<GenerationResult> out(n);
+    for (size_t i = 0; i < n; ++i) {
+        out[i].codes.assign(codes.begin() + i * stride, codes.begin() + i * stride + lengths[i]);
+        out[i].stopped = stopped[i] != 0;
+    }
+    return out;
 }
 
 GptState GptDecoder::checkpoint() const {

@@ -135,5 +135,19 @@ int main(int argc, char** argv) {
     std::printf("{\"beam_codes\":%zu,\"beam_stopped\":%d}\n", rb.codes.size(), rb.stopped ? 1 : 0);
     auto scores = itts25::apply_gpt_sampling_processors(std::vector<float>(8194, 0.5f), {1, 8192}, itts25::GenerationOptions{});
     std::printf("{\"processed\":%zu}\n", scores.size());
+    // NativeRuntime's segment loop (native_runtime.cpp:98-99) in one call, against the loop itself
+    const std::vector<std::vector<uint32_t>> segments{{5, 17, 300}, {42, 43, 44, 45, 46}, {7}};
+    itts25::GenerationOptions so;
+    so.seed = 11;
+    so.top_k = 0;
+    auto batched = gpt.generate_segments(speaker, emotion, segments, 3, so, 10);
+    bool same = batched.size() == segments.size();
+    for (size_t i = 0; same && i < segments.size(); ++i) {
+        auto o = so;
+        o.seed += i;
+        auto single = gpt.generate(gpt.prepare(speaker, emotion, segments[i], 3), o, 10);
+        same = single.codes == batched[i].codes && single.stopped == batched[i].stopped;
+    }
+    std::printf("{\"segments\":%zu,\"segments_equal_loop\":%d}\n", batched.size(), same ? 1 : 0);
     return 0;
 }

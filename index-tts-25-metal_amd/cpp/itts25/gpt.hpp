@@ -70,6 +70,14 @@ public:
     std::vector<float> prefill(const std::vector<float>& prefix);
     std::vector<float> step(uint32_t code, uint32_t position);
     GenerationResult generate(const std::vector<float>& prefix, const GenerationOptions& options, uint32_t max_tokens = 1500);
+    // The GPT part of NativeRuntime::synthesize's segment loop (src/native_runtime.cpp:98-99)
+    // for all of a request's text segments at once: result i equals
+    // generate(prepare(speaker, emotion, segments[i], language), options with seed + i,
+    // max_tokens).  No counterpart among the reference's members: it replaces that loop's
+    // prepare/generate calls, decoding the segments together on the device.
+    std::vector<GenerationResult> generate_segments(const std::vector<float>& speaker, const std::vector<float>& emotion,
+                                                    const std::vector<std::vector<uint32_t>>& segments, uint32_t language,
+                                                    const GenerationOptions& options, uint32_t max_tokens = 1500);
     GptState checkpoint() const;
     void restore(const GptState& state);
     uint32_t cached_tokens() const;

@@ -131,6 +131,8 @@ struct Engine {
     DevBuf<uint32_t> codes, status, d_parent;
     DevBuf<SeqState> state;  // kMaxBatch + 1 entries; the last one serves the processor/sampler API
     DevBuf<uint8_t> seen, seen_tmp, table, table_tmp;
+    DevBuf<float> seg_cond;     // conditioning rows shared by a request's segments
+    DevBuf<uint32_t> seg_ids;   // the segments' wrapped text ids
     DevBuf<double> probs;
     // prefill scratch
     DevBuf<float> px, pxn, pq, patt, pff;
@@ -597,8 +599,10 @@ struct Engine {
         std::vector<uint32_t> slot(M), pos(M), last(kMaxBatch, 0);
         uint32_t m = 0;
         for (int b = 0; b < nseq; ++b) {
-            HIP_CHECK(hipMemcpyAsync(px.p + static_cast<size_t>(m) * kWidth, prefixes[b], static_cast<size_t>(rows[b]) * kWidth * 4,
-                                     hipMemcpyHostToDevice, stream));
+            // a null prefix: its rows were staged in px on the device (generate_segments)
+            if (prefixes[b])
+                HIP_CHECK(hipMemcpyAsync(px.p + static_cast<size_t>(m) * kWidth, prefixes[b], static_cast<size_t>(rows[b]) * kWidth * 4,
+                                         hipMemcpyHostToDevice, stream));
             for (uint32_t r = 0; r < rows[b]; ++r) {
                 slot[m + r] = static_cast<uint32_t>(b);
                 pos[m + r] = r;
@@ -830,6 +834,9 @@ struct Engine {
 
     void generate(const float* prefix, uint32_t rows, const itts_gen_options& opt, uint32_t max_tokens, uint32_t* codes_out,
                   uint32_t* n_codes, int32_t* stopped);
+    void generate_segments(const float* cond, uint32_t n_cond, const float* speaker, const float* emotion, const uint32_t* ids,
+                           const uint32_t* id_counts, uint32_t nseg, uint32_t language, const itts_gen_options& options,
+                           uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped);
 
     // ---------------------------------------------------------------- processors / sampler API
     void apply_processors(const float* in, uint32_t vocab, const uint32_t* history, uint32_t n_history,
@@ -1083,6 +1090,91 @@ void Engine::generate(const float* prefix, uint32_t rows, const itts_gen_options
         return;
     }
     generate_batch({prefix}, {rows}, {c}, max_tokens, codes_out, n_codes, stopped);
+}
+
+// NativeRuntime::synthesize's GPT loop (native_runtime.cpp:98-99): segment i's prefix is
+// prepare(conditioning, ids_i, language) (gpt.cpp:42-71) and its codes are
+// generate(prefix, options with seed + i, max_tokens).  Every segment is checked, in order,
+// before any work is queued.  The prefixes are built on the device straight into the
+// prefill input (no host copy of the rows), and the segments are decoded together,
+// max_batch at a time; each gets the codes it gets alone (the batched forward gives every
+// row its batch-1 result).  Beam search decodes one segment at a time, as generate() does.
+void Engine::generate_segments(const float* cond, uint32_t n_cond, const float* speaker, const float* emotion, const uint32_t* ids,
+                               const uint32_t* id_counts, uint32_t nseg, uint32_t language, const itts_gen_options& options,
+                               uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
+    if (!nseg) throw std::invalid_argument("Invalid segment count");
+    std::vector<std::vector<uint32_t>> tails(nseg);
+    std::vector<uint32_t> rows(nseg);
+    std::vector<itts_gen_options> opts(nseg, options);
+    size_t off = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        prepare_tail(ids + off, id_counts[i], language, tails[i]);
+        off += id_counts[i];
+        rows[i] = n_cond + static_cast<uint32_t>(tails[i].size()) + 1;
+        check_prefix(rows[i]);
+        opts[i].seed = options.seed + i;  // native_runtime.cpp:98 (opts.seed += index)
+        validate_generation(opts[i], max_tokens, rows[i], mel_pos_rows, cap);
+    }
+    // The conditioning rows, once for all segments.
+    seg_cond.ensure(static_cast<size_t>(n_cond) * kWidth);
+    if (cond) {
+        HIP_CHECK(hipMemcpyAsync(seg_cond.p, cond, static_cast<size_t>(n_cond) * kWidth * 4, hipMemcpyHostToDevice, stream));
+    } else {
+        DevBuf<float> sp, em;
+        sp.alloc(192);
+        em.alloc(kWidth);
+        HIP_CHECK(hipMemcpyAsync(sp.p, speaker, 192 * 4, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(em.p, emotion, kWidth * 4, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipMemsetAsync(seg_cond.p, 0, static_cast<size_t>(n_cond) * kWidth * 4, stream));
+        HIP_CHECK(launch_speaker_row(spk_w.p, spk_b.p, sp.p, em.p, seg_cond.p, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));  // sp and em are freed at the end of this block
+    }
+    // Segments i0 .. i0 + n - 1: their prefixes staged back to back in px.
+    auto stage = [&](uint32_t i0, uint32_t n) {
+        size_t m = 0, nid = 0;
+        for (uint32_t i = i0; i < i0 + n; ++i) {
+            m += rows[i];
+            nid += tails[i].size();
+        }
+        px.ensure(m * kWidth);
+        seg_ids.ensure(nid);
+        std::vector<uint32_t> flat;
+        flat.reserve(nid);
+        for (uint32_t i = i0; i < i0 + n; ++i) flat.insert(flat.end(), tails[i].begin(), tails[i].end());
+        HIP_CHECK(hipMemcpyAsync(seg_ids.p, flat.data(), nid * 4, hipMemcpyHostToDevice, stream));
+        size_t r = 0, k = 0;
+        for (uint32_t i = i0; i < i0 + n; ++i) {
+            float* dst = px.p + r * kWidth;
+            HIP_CHECK(hipMemcpyAsync(dst, seg_cond.p, static_cast<size_t>(n_cond) * kWidth * 4, hipMemcpyDeviceToDevice, stream));
+            HIP_CHECK(launch_text_rows(text_emb.p, text_pos.p, lang_emb.p, mel_emb.p, mel_pos.p, seg_ids.p + k,
+                                       static_cast<int>(tails[i].size()), language, dst + static_cast<size_t>(n_cond) * kWidth, stream));
+            r += rows[i];
+            k += tails[i].size();
+        }
+        HIP_CHECK(hipStreamSynchronize(stream));  // `flat` is read by the copy above
+    };
+    float prefill_ms = 0, decode_ms = 0;
+    uint32_t steps = 0;
+    const uint32_t group = options.num_beams > 1 ? 1u : max_batch;
+    for (uint32_t i0 = 0; i0 < nseg; i0 += group) {
+        const uint32_t n = std::min(group, nseg - i0);
+        stage(i0, n);
+        uint32_t* out = codes_out + static_cast<size_t>(i0) * max_tokens;
+        if (options.num_beams > 1) {
+            generate(nullptr, rows[i0], opts[i0], max_tokens, out, n_codes + i0, stopped + i0);
+        } else {
+            const std::vector<const float*> staged(n, nullptr);
+            generate_batch(staged, std::vector<uint32_t>(rows.begin() + i0, rows.begin() + i0 + n),
+                           std::vector<itts_gen_options>(opts.begin() + i0, opts.begin() + i0 + n), max_tokens, out, n_codes + i0,
+                           stopped + i0);
+        }
+        prefill_ms += timing.prefill_ms;
+        decode_ms += timing.decode_ms;
+        steps += timing.decode_steps;
+    }
+    timing.prefill_ms = prefill_ms;
+    timing.decode_ms = decode_ms;
+    timing.decode_steps = steps;
 }
 
 // gpt_sampling.cpp:190-245.  Scores, processors and candidate selection run on the device
@@ -1354,7 +1446,10 @@ int itts_gpt_prepare_cond(itts_gpt* h, const float* cond, uint32_t n_cond, const
 }
 
 int itts_gpt_prefill(itts_gpt* h, const float* prefix, uint32_t rows, float* logits) {
-    return guarded(h, [&] { h->e.prefill(prefix, rows, logits); });
+    return guarded(h, [&] {
+        if (!prefix) throw std::invalid_argument("Invalid GPT prefill dimensions");
+        h->e.prefill(prefix, rows, logits);
+    });
 }
 
 int itts_gpt_step(itts_gpt* h, uint32_t code, uint32_t position, float* logits) {
@@ -1383,7 +1478,10 @@ void itts_gpt_state_release(itts_gpt_state* state) { delete state; }
 
 int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options, uint32_t max_tokens,
                       uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
-    return guarded(h, [&] { h->e.generate(prefix, rows, *options, max_tokens, codes_out, n_codes, stopped); });
+    return guarded(h, [&] {
+        if (!prefix) throw std::invalid_argument("Invalid GPT prefill dimensions");
+        h->e.generate(prefix, rows, *options, max_tokens, codes_out, n_codes, stopped);
+    });
 }
 
 int itts_gpt_generate_batch(itts_gpt* h, uint32_t batch, const float* const* prefixes, const uint32_t* rows,
@@ -1391,9 +1489,31 @@ int itts_gpt_generate_batch(itts_gpt* h, uint32_t batch, const float* const* pre
                             int32_t* stopped) {
     return guarded(h, [&] {
         std::vector<const float*> p(prefixes, prefixes + batch);
+        for (const float* x : p)
+            if (!x) throw std::invalid_argument("Invalid GPT prefill dimensions");
         std::vector<uint32_t> r(rows, rows + batch);
         std::vector<itts_gen_options> o(options, options + batch);
         h->e.generate_batch(p, r, o, max_tokens, codes_out, n_codes, stopped);
+    });
+}
+
+int itts_gpt_generate_segments(itts_gpt* h, const float* speaker, const float* emotion, const uint32_t* ids,
+                               const uint32_t* id_counts, uint32_t n_segments, uint32_t language, const itts_gen_options* options,
+                               uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
+    return guarded(h, [&] {
+        if (!h->e.has_speaker || !speaker || !emotion) throw std::invalid_argument("Invalid GPT conditioning dimensions");
+        h->e.generate_segments(nullptr, 3, speaker, emotion, ids, id_counts, n_segments, language, *options, max_tokens, codes_out,
+                               n_codes, stopped);
+    });
+}
+
+int itts_gpt_generate_segments_cond(itts_gpt* h, const float* cond, uint32_t n_cond, const uint32_t* ids, const uint32_t* id_counts,
+                                    uint32_t n_segments, uint32_t language, const itts_gen_options* options, uint32_t max_tokens,
+                                    uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
+    return guarded(h, [&] {
+        if (!cond || !n_cond) throw std::invalid_argument("Invalid GPT conditioning dimensions");
+        h->e.generate_segments(cond, n_cond, nullptr, nullptr, ids, id_counts, n_segments, language, *options, max_tokens, codes_out,
+                               n_codes, stopped);
     });
 }
 

@@ -97,6 +97,10 @@ def _load() -> C.CDLL:
         "itts_gpt_state_release": (None, [P]),
         "itts_gpt_generate": (C.c_int, [P, f32p, u32, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
         "itts_gpt_generate_batch": (C.c_int, [P, u32, C.POINTER(f32p), u32p, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
+        "itts_gpt_generate_segments": (C.c_int, [P, f32p, f32p, u32p, u32p, u32, u32, C.POINTER(_Options), u32, u32p, u32p,
+                                                 C.POINTER(i32)]),
+        "itts_gpt_generate_segments_cond": (C.c_int, [P, f32p, u32, u32p, u32p, u32, u32, C.POINTER(_Options), u32, u32p, u32p,
+                                                      C.POINTER(i32)]),
         "itts_gpt_apply_processors": (C.c_int, [P, f32p, u32, u32p, u32, C.POINTER(_Options), f32p]),
         "itts_gpt_sample": (C.c_int, [P, f32p, u32, C.POINTER(C.c_uint64), u32, u32p]),
         "itts_gpt_last_timing": (C.c_int, [P, C.POINTER(_Timing)]),
@@ -414,6 +418,44 @@ class GptDecoder:
         self._check(_lib.itts_gpt_generate_batch(self._h, B, ptrs, _up(rows), copts, int(max_tokens), _up(codes), _up(n),
                                                  stopped.ctypes.data_as(C.POINTER(C.c_int32))))
         return [GenerationResult([int(c) for c in codes[b, : n[b]]], bool(stopped[b])) for b in range(B)]
+
+    @staticmethod
+    def _segments(segments: Sequence[Sequence[int]]):
+        counts = np.array([len(x) for x in segments], np.uint32)
+        flat = np.concatenate([np.asarray(x, dtype=np.uint32).reshape(-1) for x in segments]) if len(segments) else \
+            np.zeros(0, np.uint32)
+        return np.ascontiguousarray(flat, dtype=np.uint32), counts
+
+    def _segment_results(self, fn, args, nseg: int, options, max_tokens: int) -> List[GenerationResult]:
+        codes = np.zeros((max(1, nseg), max(1, int(max_tokens))), np.uint32)
+        n = np.zeros(max(1, nseg), np.uint32)
+        stopped = np.zeros(max(1, nseg), np.int32)
+        o = options._c()
+        self._check(fn(self._h, *args, C.byref(o), int(max_tokens), _up(codes), _up(n), stopped.ctypes.data_as(C.POINTER(C.c_int32))))
+        return [GenerationResult([int(c) for c in codes[i, : n[i]]], bool(stopped[i])) for i in range(nseg)]
+
+    def generate_segments(self, speaker: np.ndarray, emotion: np.ndarray, segments: Sequence[Sequence[int]], language: int,
+                          options: "GenerationOptions", max_tokens: int = 1500) -> List[GenerationResult]:
+        """NativeRuntime::synthesize's GPT loop (native_runtime.cpp:98-99) for a request's text
+        segments: segment i is prepare(speaker, emotion, segments[i], language) then generate()
+        with options.seed + i; all segments are decoded together on the device."""
+        sp = np.ascontiguousarray(speaker, dtype=np.float32)
+        em = np.ascontiguousarray(emotion, dtype=np.float32)
+        if sp.size != 192 or em.size != WIDTH:
+            raise InvalidArgument("Invalid GPT conditioning dimensions")
+        flat, counts = self._segments(segments)
+        return self._segment_results(_lib.itts_gpt_generate_segments,
+                                     (_fp(sp), _fp(em), _up(flat), _up(counts), len(counts), int(language)), len(counts), options,
+                                     max_tokens)
+
+    def generate_segments_cond(self, cond: np.ndarray, segments: Sequence[Sequence[int]], language: int,
+                               options: "GenerationOptions", max_tokens: int = 1500) -> List[GenerationResult]:
+        """generate_segments() with the conditioning rows given directly (as prepare_cond)."""
+        cd = np.ascontiguousarray(cond, dtype=np.float32).reshape(-1, WIDTH)
+        flat, counts = self._segments(segments)
+        return self._segment_results(_lib.itts_gpt_generate_segments_cond,
+                                     (_fp(cd), cd.shape[0], _up(flat), _up(counts), len(counts), int(language)), len(counts),
+                                     options, max_tokens)
 
     def checkpoint(self) -> GptState:
         ptr = C.c_void_p()

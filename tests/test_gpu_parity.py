@@ -179,6 +179,68 @@ def test_batch_generate_matches_single_and_oracle(small, itts, oracle):
         assert batch[b].codes == codes
 
 
+def _segment_case(itts, n, seed):
+    rng = np.random.default_rng(seed)
+    segments = [[int(x) for x in rng.integers(0, 12000, int(rng.integers(1, 40)))] for _ in range(n)]
+    segments[min(2, n - 1)] = [0, 1, 5]  # prepare drops ids 0 and 1
+    return segments
+
+
+@pytest.mark.parametrize("opts", [
+    dict(seed=77),
+    dict(do_sample=False, repetition_penalty=1.0),
+    dict(seed=5, num_beams=3),
+])
+def test_generate_segments_equal_loop_and_oracle(small_weights, itts, oracle, opts):
+    """NativeRuntime::synthesize's segment loop (native_runtime.cpp:98-99): segment i's codes
+    are those of prepare(speaker, emotion, ids_i) + generate(options with seed + i), both on
+    the GPU and in the oracle.  Five segments on a max_batch 2 decoder: groups of 2, 2, 1
+    (beam search: one segment at a time)."""
+    import dataclasses
+
+    dec = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=3 if opts.get("num_beams") else 2)
+    orc = oracle.OracleGpt(small_weights, kv_capacity=1024)
+    sp, em = itts.synthetic_normal(192, 31), itts.synthetic_normal(1280, 32)
+    segments = _segment_case(itts, 5, 21)
+    o = itts.GenerationOptions(**opts)
+    print(f"segments: {opts}", flush=True)
+    got = dec.generate_segments(sp, em, segments, 3, o, 24)
+    assert len(got) == 5
+    for i, seg in enumerate(segments):
+        oi = dataclasses.replace(o, seed=o.seed + i)
+        single = dec.generate(dec.prepare(sp, em, seg, 3), oi, 24)
+        assert (got[i].codes, got[i].stopped) == (single.codes, single.stopped), i
+        codes, stopped = orc.generate(orc.prepare(sp, em, seg, 3), oracle.options_from(oi), 24)
+        assert (got[i].codes, got[i].stopped) == (codes, stopped), i
+    dec.close()
+
+
+def test_generate_segments_cond_and_errors(small_weights, itts):
+    """The raw-conditioning form equals prepare_cond + generate per segment; argument errors
+    carry prepare's and generate's messages, checked for every segment before any work."""
+    import dataclasses
+
+    dec = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=4)
+    cond, _ = itts.synthetic_prefix_inputs(4, seed=8)
+    segments = _segment_case(itts, 3, 9)
+    o = itts.GenerationOptions(seed=123, suppress_stop=True)
+    got = dec.generate_segments_cond(cond, segments, 0, o, 30)
+    for i, seg in enumerate(segments):
+        single = dec.generate(dec.prepare_cond(cond, seg, 0), dataclasses.replace(o, seed=o.seed + i), 30)
+        assert (got[i].codes, got[i].stopped) == (single.codes, single.stopped), i
+        assert len(got[i].codes) == 30
+    sp, em = itts.synthetic_normal(192, 1), itts.synthetic_normal(1280, 2)
+    with pytest.raises(itts.InvalidArgument, match="Invalid segment count"):
+        dec.generate_segments(sp, em, [], 0, o, 8)
+    with pytest.raises(itts.InvalidArgument, match="Text token is outside 2.5 vocabulary"):
+        dec.generate_segments(sp, em, [[5, 6], [12000]], 0, o, 8)
+    with pytest.raises(itts.InvalidArgument, match="GPT generation capacity exceeded"):
+        dec.generate_segments(sp, em, [[5, 6], [7]], 0, o, 1020)  # 8 + 1020 rows >= capacity 1024
+    with pytest.raises(itts.InvalidArgument, match="Invalid GPT conditioning dimensions"):
+        dec.generate_segments(sp[:10], em, [[5]], 0, o, 8)
+    dec.close()
+
+
 def test_generate_argument_errors(small, itts):
     dec, _, cond, text = small
     prefix = dec.prepare_cond(cond, text, 0)

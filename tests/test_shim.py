@@ -27,6 +27,7 @@ def test_shim_runs_on_gpu():
     assert lines[0]["codes"] + lines[0]["stopped"] >= 1
     assert lines[1]["beam_codes"] + lines[1]["beam_stopped"] >= 1
     assert lines[2]["processed"] == 8194
+    assert lines[3] == {"segments": 3, "segments_equal_loop": 1}
 
 
 @pytest.mark.gpu

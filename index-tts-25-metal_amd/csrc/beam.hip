@@ -12,7 +12,9 @@
 //   replacement with sample_gpt_token_from_logits (:217-222), by wave 0 alone with the
 //   finite candidates in LDS when there are at most kLdsCands of them (each draw's sums
 //   lane-serial in index order); then a stable sort of the candidates by score (:228).
-// The host reads the candidates and runs the reference's child/finish bookkeeping.
+// beam_children_kernel picks the children on the device (the next forward is queued without
+// waiting for the host); the host reads the candidates a step or two later and runs the
+// reference's child/finish bookkeeping.
 #include "sampler_dev.h"
 
 namespace itts {
@@ -27,6 +29,10 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     __shared__ float wred[NWAVE];
     __shared__ float log_sum_s;
     const int p = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (a.parents_dev && p >= static_cast<int>(*a.parents_dev)) {  // the whole workgroup leaves together
+        if (t == 0) a.status[1 + p] = kOk;
+        return;
+    }
     const float* lg = a.logits + static_cast<size_t>(p) * V;
     float* e = reinterpret_cast<float*>(sm.sortbuf) + V + 2;  // after s[] inside the union, 16-byte aligned
     float mloc = -INFINITY;
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     __shared__ float mx_s;
     __shared__ uint32_t stop_s;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n = a.parents * V;
+    const int n = (a.parents_dev ? static_cast<int>(*a.parents_dev) : a.parents) * V;
     const float* S = a.all_scores;
     const int take = a.take;
     const int chunk = (n + NT - 1) / NT;
@@ -395,7 +401,51 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     }
 }
 
+// One thread: at most 2 * 10 candidates and 10 children.
+__global__ void beam_children_kernel(const BeamCand* cand, int take, int beams, uint32_t* parents_dev, uint32_t* parent, uint32_t* token,
+                                     float* score, SeqState* state, const SeqState* tmpl, uint32_t n, uint32_t position) {
+    if (threadIdx.x != 0) return;
+    const uint32_t P = *parents_dev;
+    int C = 0;
+    for (int r = 0; r < take && C < beams; ++r) {
+        const BeamCand c = cand[r];
+        if (c.token == static_cast<uint32_t>(kMelStop)) continue;
+        if (c.token >= static_cast<uint32_t>(kMelStart) || c.parent >= P) {
+            C = 0;
+            break;
+        }
+        parent[C] = c.parent;
+        token[C] = c.token;
+        score[C] = c.score;
+        ++C;
+    }
+    for (int c = 0; c < beams; ++c) {
+        SeqState st = *tmpl;
+        st.n = n;
+        st.position = position;
+        if (c < C) {
+            st.token = token[c];
+        } else {
+            parent[c] = 0;
+            token[c] = 0;
+            score[c] = -INFINITY;
+            st.token = 0;
+            st.active = 0;
+        }
+        state[c] = st;
+    }
+    *parents_dev = C > 0 ? static_cast<uint32_t>(C) : 1u;
+}
+
 }  // namespace
+
+hipError_t launch_beam_children(const BeamCand* cand, int take, int beams, uint32_t* parents_dev, uint32_t* parent, uint32_t* token,
+                                float* score, SeqState* state, const SeqState* tmpl, uint32_t n, uint32_t position, hipStream_t s) {
+    if (take < 1 || take > kMaxBeamTake || beams < 1 || beams > kMaxBatch) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(beam_children_kernel, dim3(1), dim3(64), 0, s, cand, take, beams, parents_dev, parent, token, score, state, tmpl, n,
+                       position);
+    return hipGetLastError();
+}
 
 hipError_t launch_beam_scores(const BeamArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(beam_scores_kernel, dim3(a.parents), dim3(NT), 0, s, a);

@@ -173,9 +173,19 @@ struct BeamArgs {
     int parents, take, do_sample, suppress_stop;
     float temperature, top_p, penalty;
     uint32_t top_k, num_beams;
+    const uint32_t* parents_dev;  // the step's parent count on the device (<= parents), or null: parents
 };
 hipError_t launch_beam_scores(const BeamArgs& a, hipStream_t s);
 hipError_t launch_beam_select(const BeamArgs& a, hipStream_t s);
+// Children of a beam step on the device (gpt_sampling.cpp:229-236): from the ranked
+// candidates, skipping stop tokens, the first `beams` become children 0, 1, ... with
+// parent[c], token[c], score[c] (the next step's parent scores) and state[c] (tmpl with
+// n, position and token[c]).  Slots without a child, and every slot when a candidate is out
+// of range (a code >= 8192 or a parent >= *parents_dev: the host raises at that step), are
+// inactive with parent 0 and token 0.  *parents_dev becomes the child count, at least 1.
+hipError_t launch_beam_children(const BeamCand* cand, int take, int beams, uint32_t* parents_dev, uint32_t* parent,
+                                uint32_t* token, float* score, SeqState* state, const SeqState* tmpl, uint32_t n, uint32_t position,
+                                hipStream_t s);
 
 // ------------------------------------------------------------------ prefill
 struct LnRowsArgs {

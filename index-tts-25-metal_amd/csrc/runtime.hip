@@ -143,6 +143,17 @@ struct Engine {
     DevBuf<double> beam_probs;
     DevBuf<BeamCand> cand;
     DevBuf<uint64_t> beam_rng;
+    DevBuf<uint32_t> beam_np;    // the step's parent count, advanced by beam_children_kernel
+    DevBuf<SeqState> beam_tmpl;  // decode state of a child, before its n, position and token
+    // Candidates and statuses of a queued beam step, read back into pinned memory; the host
+    // runs up to kBeamLag steps behind the device.
+    struct BeamSlot {
+        BeamCand cand[kMaxBeamTake];
+        uint32_t status[1 + kMaxBatch];
+    };
+    static constexpr uint32_t kBeamRing = 4, kBeamLag = 2;
+    BeamSlot* beam_ring = nullptr;
+    hipEvent_t bev[kBeamRing] = {};
     // API scratch
     DevBuf<float> api_out;
     DevBuf<uint32_t> api_tokens;
@@ -171,6 +182,9 @@ struct Engine {
         for (auto& kvp : graphs) (void)hipGraphExecDestroy(kvp.second);
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
+        for (auto& e : bev)
+            if (e) (void)hipEventDestroy(e);
+        if (beam_ring) (void)hipHostFree(beam_ring);
         if (pinned) (void)hipHostFree(pinned);
         if (pinned_state) (void)hipHostFree(pinned_state);
         if (stream) (void)hipStreamDestroy(stream);
@@ -1178,9 +1192,15 @@ void Engine::generate_segments(const float* cond, uint32_t n_cond, const float* 
 }
 
 // gpt_sampling.cpp:190-245.  Scores, processors and candidate selection run on the device
-// (beam.hip); the child/finish bookkeeping below is the reference's, on the host.  Beam
-// KV is not snapshotted: child c lives in slot c and inherits its parent's rows through
-// the row-owner table (one byte per row), which the attention kernel gathers through.
+// (beam.hip); so does the choice of children (beam_children_kernel applies the rule of
+// :229-236 to the ranked candidates), so every step (scores, selection, children, KV
+// reorder, forward) is queued without waiting for the host.  The host reads each step's
+// candidates back a step or two later and runs the reference's child/finish bookkeeping
+// on them, with the same rule, so its beams are the device's children.  When the search
+// ends (early stop, no children, an error), up to kBeamLag queued steps are discarded.
+// Beam KV is not snapshotted: child c lives in slot c and inherits its parent's rows
+// through the row-owner table (one byte per row), which the attention kernels gather
+// through.  Every forward runs num_beams rows; slots without a child are inactive.
 void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_options& config, uint32_t maximum,
                             std::vector<uint32_t>& result, bool& eos) {
     const uint32_t nbeam = config.num_beams;
@@ -1204,6 +1224,14 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
     cand.ensure(kMaxBeamTake);
     d_token.ensure(kMaxBatch);
     beam_rng.ensure(1);
+    beam_np.ensure(1);
+    beam_tmpl.ensure(1);
+    if (!beam_ring) {
+        HIP_CHECK(hipHostMalloc(&beam_ring, kBeamRing * sizeof(BeamSlot), hipHostMallocDefault));
+        for (auto& e : bev) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    const int nb = gemv_batch_bucket(static_cast<int>(nbeam));
+    if (use_graphs && !persistent(static_cast<int>(nbeam), true)) (void)graph(static_cast<int>(nbeam), nb, false, true);
 
     pinned_state[0] = make_state(config, rows, maximum);
     upload_states(1);
@@ -1214,27 +1242,22 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
     HIP_CHECK(hipMemsetAsync(table.p, 0, static_cast<size_t>(nbeam) * cap, stream));  // prefix rows live in slot 0
     HIP_CHECK(hipEventRecord(ev[1], stream));
     reset_seen(static_cast<int>(nbeam));
+    // The initial beams (gpt_sampling.cpp:196-198): nbeam parents sharing the prefill logits,
+    // scores 0, -1e9, ...; the search's RNG; the children's state template.
     uint64_t* prng = reinterpret_cast<uint64_t*>(pinned + 62);
     *prng = config.seed;
+    float* pscore = reinterpret_cast<float*>(pinned + 32);
+    for (uint32_t p = 0; p < nbeam; ++p) pscore[p] = p ? -1e9f : 0.0f;
+    pinned[48] = nbeam;
     HIP_CHECK(hipMemcpyAsync(beam_rng.p, prng, 8, hipMemcpyHostToDevice, stream));
+    HIP_CHECK(hipMemcpyAsync(beam_scores.p, pscore, nbeam * 4, hipMemcpyHostToDevice, stream));
+    HIP_CHECK(hipMemcpyAsync(beam_np.p, pinned + 48, 4, hipMemcpyHostToDevice, stream));
+    HIP_CHECK(hipMemcpyAsync(beam_tmpl.p, pinned_state, sizeof(SeqState), hipMemcpyHostToDevice, stream));
 
-    std::vector<Beam> beams(nbeam);
-    for (uint32_t i = 1; i < beams.size(); ++i) beams[i].score = -1e9f;
-    auto finish = [&](const Beam& beam, float score, uint32_t length, bool e) {
-        finished.push_back({beam.codes, score / std::pow(static_cast<double>(std::max(length, 1u)), config.length_penalty), e});
-        std::stable_sort(finished.begin(), finished.end(), [](const auto& x, const auto& y) { return x.score > y.score; });
-        if (finished.size() > nbeam) finished.resize(nbeam);
-    };
-    uint32_t last_rows = rows, steps = 0;
-    std::vector<BeamCand> cands(take);
-    std::vector<uint32_t> st(1 + kMaxBatch);
-    float* pscore = reinterpret_cast<float*>(pinned + 52);
-    uint32_t* ppar = pinned + 32;
-    uint32_t* ptok = pinned + 42;
-    for (uint32_t step_index = 0; step_index < maximum; ++step_index) {
-        const uint32_t P = static_cast<uint32_t>(beams.size());
-        for (uint32_t p = 0; p < P; ++p) pscore[p] = beams[p].score;
-        HIP_CHECK(hipMemcpyAsync(beam_scores.p, pscore, P * 4, hipMemcpyHostToDevice, stream));
+    // Step k: scores and selection over the current parents, the candidates read back into
+    // ring slot k, then (unless it is the last step) the children, their KV rows and repetition
+    // sets, and their forward.
+    auto enqueue = [&](uint32_t k) {
         BeamArgs a{};
         a.logits = logits.p;
         a.seen = seen.p;
@@ -1245,7 +1268,8 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
         a.status = status.p;
         a.rng = beam_rng.p;
         a.cand = cand.p;
-        a.parents = static_cast<int>(P);
+        a.parents = static_cast<int>(nbeam);
+        a.parents_dev = beam_np.p;
         a.take = static_cast<int>(take);
         a.do_sample = config.do_sample ? 1 : 0;
         a.suppress_stop = config.suppress_stop ? 1 : 0;
@@ -1256,13 +1280,38 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
         a.num_beams = nbeam;
         HIP_CHECK(launch_beam_scores(a, stream));
         HIP_CHECK(launch_beam_select(a, stream));
-        HIP_CHECK(hipMemcpyAsync(cands.data(), cand.p, take * sizeof(BeamCand), hipMemcpyDeviceToHost, stream));
-        HIP_CHECK(hipMemcpyAsync(st.data(), status.p, (1 + P) * 4, hipMemcpyDeviceToHost, stream));
-        HIP_CHECK(hipStreamSynchronize(stream));
+        BeamSlot& slot = beam_ring[k % kBeamRing];
+        HIP_CHECK(hipMemcpyAsync(slot.cand, cand.p, take * sizeof(BeamCand), hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipMemcpyAsync(slot.status, status.p, (1 + nbeam) * 4, hipMemcpyDeviceToHost, stream));
+        if (k + 1 < maximum) {
+            const uint32_t n = rows + k;  // rows cached before this forward, equal for every beam
+            HIP_CHECK(launch_beam_children(cand.p, static_cast<int>(take), static_cast<int>(nbeam), beam_np.p, d_parent.p, d_token.p,
+                                           beam_scores.p, state.p, beam_tmpl.p, n, k + 2, stream));
+            HIP_CHECK(launch_beam_reorder(table.p, table_tmp.p, seen.p, seen_tmp.p, d_parent.p, d_token.p, static_cast<int>(nbeam),
+                                          static_cast<int>(nbeam), n, cap, stream));
+            run_step(static_cast<int>(nbeam), nb, false, true);
+        }
+        HIP_CHECK(hipEventRecord(bev[k % kBeamRing], stream));
+    };
+
+    std::vector<Beam> beams(nbeam);
+    for (uint32_t i = 1; i < beams.size(); ++i) beams[i].score = -1e9f;
+    auto finish = [&](const Beam& beam, float score, uint32_t length, bool e) {
+        finished.push_back({beam.codes, score / std::pow(static_cast<double>(std::max(length, 1u)), config.length_penalty), e});
+        std::stable_sort(finished.begin(), finished.end(), [](const auto& x, const auto& y) { return x.score > y.score; });
+        if (finished.size() > nbeam) finished.resize(nbeam);
+    };
+    uint32_t last_rows = rows, steps = 0, queued = 0;
+    std::vector<BeamCand> cands(take);
+    for (uint32_t step_index = 0; step_index < maximum; ++step_index) {
+        while (queued < maximum && queued <= step_index + kBeamLag) enqueue(queued++);
+        HIP_CHECK(hipEventSynchronize(bev[step_index % kBeamRing]));
+        const BeamSlot& slot = beam_ring[step_index % kBeamRing];
+        const uint32_t P = static_cast<uint32_t>(beams.size());
         for (uint32_t i = 0; i <= P; ++i)
-            if (st[i]) throw std::runtime_error(sampler_message(st[i]));
+            if (slot.status[i]) throw std::runtime_error(sampler_message(slot.status[i]));
+        std::copy(slot.cand, slot.cand + take, cands.begin());
         std::vector<Beam> next;
-        uint32_t C = 0;
         for (uint32_t rank = 0; rank < take; ++rank) {
             const BeamCand c = cands[rank];
             const Beam& parent = beams[c.parent];
@@ -1275,29 +1324,12 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
             child.codes = parent.codes;
             child.codes.push_back(c.token);
             child.score = c.score;
-            ppar[C] = c.parent;
-            ptok[C] = c.token;
-            ++C;
             next.push_back(std::move(child));
             if (next.size() == nbeam) break;
         }
         if (next.empty()) break;
-        if (step_index + 1 < maximum) {
-            const uint32_t n = rows + step_index;  // rows cached before this forward, equal for every beam
-            HIP_CHECK(hipMemcpyAsync(d_parent.p, ppar, C * 4, hipMemcpyHostToDevice, stream));
-            HIP_CHECK(hipMemcpyAsync(d_token.p, ptok, C * 4, hipMemcpyHostToDevice, stream));
-            HIP_CHECK(launch_beam_reorder(table.p, table_tmp.p, seen.p, seen_tmp.p, d_parent.p, d_token.p, static_cast<int>(P),
-                                          static_cast<int>(C), n, cap, stream));
-            for (uint32_t c = 0; c < C; ++c) {
-                SeqState s = make_state(config, rows, maximum);
-                s.n = n;
-                s.position = step_index + 2;
-                s.token = ptok[c];
-                pinned_state[c] = s;
-            }
-            upload_states(static_cast<int>(C));
-            run_step(static_cast<int>(C), gemv_batch_bucket(static_cast<int>(C)), false, true);
-            last_rows = n + 1;
+        if (step_index + 1 < maximum) {  // this step's forward (queued with the step) counts
+            last_rows = rows + step_index + 1;
             ++steps;
         }
         beams = std::move(next);
@@ -1312,6 +1344,7 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
     HIP_CHECK(hipEventElapsedTime(&timing.prefill_ms, ev[0], ev[1]));
     HIP_CHECK(hipEventElapsedTime(&timing.decode_ms, ev[1], ev[2]));
     timing.decode_steps = steps;
+    check_step_error();
     for (const auto& beam : beams) finish(beam, beam.score, static_cast<uint32_t>(beam.codes.size()), false);
     if (finished.empty()) throw std::runtime_error("Beam search produced no hypotheses");
     result = std::move(finished[0].codes);

@@ -87,12 +87,33 @@ struct Snapshot {
 // A persistent step grid takes one workgroup slot on every CU and needs all of its
 // workgroups resident together.  Two such grids running at once on one GPU (decoders of
 // this process on different streams) could each hold CUs the other is waiting for, so
-// the launches on a device are chained: each waits for the previous one, whichever decoder
-// made it.  The chain is process-wide and never freed.
+// while more than one decoder on a device can launch them, the launches are chained: each
+// waits for the previous one, whichever decoder made it.  With one such decoder the chain
+// is skipped (its marker packets cost about 3 us per token).  A decoder that registers as
+// the second one drains the device first, so no unchained grid is still running when
+// chained launches begin; a decoder drains its own stream before it unregisters.
+// The chain is process-wide and never freed.
+std::mutex g_step_mu;
+std::unordered_map<int, int> g_step_users;          // device -> decoders that launch persistent grids
+std::unordered_map<int, hipEvent_t> g_step_last;    // device -> recorded after its latest chained launch
+
+void register_step_user(int dev) {
+    int users = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_step_mu);
+        users = ++g_step_users[dev];
+    }
+    if (users == 2) HIP_CHECK(hipDeviceSynchronize());
+}
+void unregister_step_user(int dev) {
+    std::lock_guard<std::mutex> lock(g_step_mu);
+    --g_step_users[dev];
+}
+
 hipError_t launch_step_serialized(const StepArgs& a, int nseq, int grid, bool bf16, int dev, hipStream_t s) {
-    static std::mutex mu;
-    static std::unordered_map<int, hipEvent_t> last;  // device -> recorded after its latest step launch
-    std::lock_guard<std::mutex> lock(mu);
+    std::lock_guard<std::mutex> lock(g_step_mu);
+    if (g_step_users[dev] <= 1) return nseq == 1 ? launch_step(a, grid, bf16, s) : launch_step_batch(a, nseq, grid, s);
+    auto& last = g_step_last;
     auto it = last.find(dev);
     if (it == last.end()) {
         hipEvent_t e = nullptr;
@@ -179,6 +200,10 @@ struct Engine {
     std::string last_error;
 
     ~Engine() {
+        if (step_ok) {
+            if (stream) (void)hipStreamSynchronize(stream);  // no grid of this decoder outlives its registration
+            unregister_step_user(step_dev);
+        }
         for (auto& kvp : graphs) (void)hipGraphExecDestroy(kvp.second);
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
@@ -379,6 +404,7 @@ struct Engine {
         step_err.alloc(1);
         HIP_CHECK(hipMemsetAsync(step_err.p, 0, sizeof(uint32_t), stream));
         step_grid = cus;
+        register_step_user(dev);
         step_ok = true;
     }
 

@@ -397,6 +397,43 @@ def test_persistent_generate_equals_multikernel(both_paths, itts):
     assert step.cached_tokens() == multi.cached_tokens()
 
 
+def test_two_decoders_concurrently_on_one_gpu(itts, small_weights):
+    """Two decoders of one process on one GPU, each driven from its own thread, both on the
+    persistent step (batch 1 and batch 2): their grids are chained, never resident together,
+    so each gets the codes it gets alone and no hand-off times out."""
+    import dataclasses
+    import threading
+
+    a = itts.GptDecoder(small_weights, kv_capacity=1024)
+    b = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=2)
+    cond, text = itts.synthetic_prefix_inputs(30, seed=12)
+    prefix = a.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(seed=3, suppress_stop=True)
+    opts = [o, dataclasses.replace(o, seed=4)]
+    ref_a = a.generate(prefix, o, 64)
+    ref_b = b.generate_batch([prefix, prefix], opts, 64)
+    assert a.last_timing()["decode_path"] == b.last_timing()["decode_path"] == "step"
+    out, errors = {}, []
+
+    def run(name, fn):
+        try:
+            out[name] = [fn() for _ in range(3)]
+        except Exception as e:  # reported below: a thread's exception is not raised by join()
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=("a", lambda: a.generate(prefix, o, 64))),
+               threading.Thread(target=run, args=("b", lambda: b.generate_batch([prefix, prefix], opts, 64)))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(120)
+    assert not errors, errors
+    assert all(r.codes == ref_a.codes for r in out["a"])
+    assert all([x.codes for x in r] == [x.codes for x in ref_b] for r in out["b"])
+    a.close()
+    b.close()
+
+
 @pytest.fixture(scope="module")
 def batch_paths(itts, small_weights):
     """The 2-layer model with its stop token made likely (mel_head bias + 2.5), on the persistent

@@ -34,6 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "index-tts-25-metal_amd"))
 
 HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix-core peak
 WEIGHT_BYTES_PER_TOKEN = 1_931_051_016  # FP32 weights + biases + LayerNorm + mel_head + 2 embedding rows
 KV_BYTES_PER_ROW = 245_760              # 24 layers x (K + V) x 1280 x 4 B
 METRIC = "GPT decode tokens/s @bs1 FP32 + % of HBM roofline; beam-3 tokens/s"
@@ -139,6 +140,15 @@ def extras(it, dec, weights):
         "loop_seconds": round(min(ltimes), 4), "loop_tokens_per_s": round(total / min(ltimes), 2),
         "same_codes_as_loop": [x.codes for x in r] == [x.codes for x in loop],
     }
+    # The consumer of the codes: EnhancedCodec::decode (codec.cpp:64-72) of 600 codes (config 2's
+    # output) and of 47 (a short utterance), random-init codec weights; GEMM FLOPs over the
+    # FP32 matrix-core peak.
+    codec = it.EnhancedCodec(it.make_synthetic_codec_weights(seed=0))
+    c600, c47 = codec.bench(600, 20), codec.bench(47, 20)
+    codec.close()
+    tf = c600["flops"] / (c600["avg_ms"] * 1e-3) / 1e12
+    res["codec_decode"] = {"codes": 600, "avg_ms": round(c600["avg_ms"], 4), "TFLOPs": round(tf, 2),
+                           "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "codes_47_avg_ms": round(c47["avg_ms"], 4)}
     for dtype in ("f32", "bf16"):
         d = dec if dtype == "f32" else it.GptDecoder(weights, kv_capacity=4096, max_batch=8, weight_dtype="bf16")
         d.generate_batch(prefixes, opts, 16)

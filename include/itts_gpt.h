@@ -210,6 +210,26 @@ int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
 int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t cached_rows, uint32_t iters, float* avg_ms,
                           double* bytes_per_launch);
 
+/* ---- EnhancedCodec (src/codec.cpp), the consumer of the semantic codes ----------
+ * The decode path of itts25::EnhancedCodec (include/itts25/codec.hpp:11-17) on the
+ * MI355X: codes -> [2T][1024] time-major features.  encode() is not provided. */
+typedef struct itts_codec itts_codec;
+/* EnhancedCodec::EnhancedCodec (codec.cpp:5-20): the decode path's tensors by their
+ * reference names (codebook, out_project, codec.decoder.*, codec.up), with the
+ * reference's "Unsupported 2.5 codec shape: <name>" check (ITTS_ERUNTIME).  Failures are
+ * reported by itts_codec_last_error(NULL) (thread local). */
+int itts_codec_create(const itts_tensor* tensors, int32_t count, itts_codec** out);
+/* The same from a MIT2 bundle's codec.* tensors (f32), uploaded from the mapping. */
+int itts_codec_create_from_bundle(const itts_bundle* b, itts_codec** out);
+void itts_codec_destroy(itts_codec* c);
+const char* itts_codec_last_error(const itts_codec* c);
+/* EnhancedCodec::decode (codec.cpp:64-72): n codes in [0, 8192), 1 <= n <= 5000
+ * ("Codec expects 1..5000 code IDs in [0,8192)", ITTS_EINVAL); out holds 2n x 1024. */
+int itts_codec_decode(itts_codec* c, const uint32_t* codes, uint32_t n, float* out);
+/* Measurement hook (no reference counterpart): mean duration of the device work of a
+ * decode of n codes over `iters` back-to-back runs (HIP events), and its GEMM FLOPs. */
+int itts_codec_bench(itts_codec* c, uint32_t n, uint32_t iters, float* avg_ms, double* flops);
+
 /* Deterministic N(mean, std^2) fill for synthetic weights and inputs: value i is
  * a Box-Muller transform of two SplitMix64 outputs keyed by (seed, i), so the
  * result does not depend on thread count.  Host only. */

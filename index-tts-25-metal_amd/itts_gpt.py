@@ -113,6 +113,12 @@ def _load() -> C.CDLL:
         "itts_bundle_tensor_at": (C.c_int, [P, i32, C.POINTER(_BundleTensor)]),
         "itts_bundle_find": (C.c_int, [P, C.c_char_p, C.POINTER(_BundleTensor)]),
         "itts_gpt_create_from_bundle": (C.c_int, [P, C.POINTER(_Config), C.POINTER(P)]),
+        "itts_codec_create": (C.c_int, [C.POINTER(_Tensor), i32, C.POINTER(P)]),
+        "itts_codec_create_from_bundle": (C.c_int, [P, C.POINTER(P)]),
+        "itts_codec_destroy": (None, [P]),
+        "itts_codec_last_error": (C.c_char_p, [P]),
+        "itts_codec_decode": (C.c_int, [P, u32p, u32, f32p]),
+        "itts_codec_bench": (C.c_int, [P, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -585,6 +591,99 @@ def make_synthetic_weights(layers: int = 24, seed: int = 0, std: float = 0.02, l
         else:
             out[name] = synthetic_normal(n, _tensor_seed(seed, name), 0.0, std).reshape(shape)
     return out
+
+
+CODEC_WIDTH, CODEC_HIDDEN, CODEC_FFN, CODEC_BLOCKS, CODEBOOK = 1024, 384, 2048, 12, 8192
+
+
+def codec_weight_shapes() -> Dict[str, tuple]:
+    """The tensors EnhancedCodec::decode reads (src/codec.cpp:5-20, 36-72), reference names."""
+    q, d = "codec.quantizer.quantizers.0", "codec.decoder.0"
+    s = {f"{q}.codebook.weight": (CODEBOOK, 8), f"{q}.out_project.weight": (CODEC_WIDTH, 8), f"{q}.out_project.bias": (CODEC_WIDTH,),
+         f"{d}.embed.weight": (CODEC_HIDDEN, CODEC_WIDTH, 7), f"{d}.embed.bias": (CODEC_HIDDEN,),
+         f"{d}.norm.weight": (CODEC_HIDDEN,), f"{d}.norm.bias": (CODEC_HIDDEN,)}
+    for i in range(CODEC_BLOCKS):
+        l = f"{d}.convnext.{i}"
+        s.update({f"{l}.dwconv.weight": (CODEC_HIDDEN, 1, 7), f"{l}.dwconv.bias": (CODEC_HIDDEN,),
+                  f"{l}.norm.weight": (CODEC_HIDDEN,), f"{l}.norm.bias": (CODEC_HIDDEN,),
+                  f"{l}.pwconv1.weight": (CODEC_FFN, CODEC_HIDDEN), f"{l}.pwconv1.bias": (CODEC_FFN,),
+                  f"{l}.pwconv2.weight": (CODEC_HIDDEN, CODEC_FFN), f"{l}.pwconv2.bias": (CODEC_HIDDEN,),
+                  f"{l}.gamma": (CODEC_HIDDEN,)})
+    s.update({f"{d}.final_layer_norm.weight": (CODEC_HIDDEN,), f"{d}.final_layer_norm.bias": (CODEC_HIDDEN,),
+              "codec.decoder.1.weight": (CODEC_WIDTH, CODEC_HIDDEN), "codec.decoder.1.bias": (CODEC_WIDTH,),
+              "codec.up.weight": (CODEC_WIDTH, CODEC_WIDTH, 3), "codec.up.bias": (CODEC_WIDTH,)})
+    return s
+
+
+def make_synthetic_codec_weights(seed: int = 0, std: float = 0.02) -> Dict[str, np.ndarray]:
+    """Random-init codec decode weights: convolutions, linears and biases N(0, std^2); codebook
+    N(0, 1); LayerNorm gamma N(1, 0.1^2), beta N(0, 0.1^2); layer scales N(0.5, 0.1^2)."""
+    out: Dict[str, np.ndarray] = {}
+    for name, shape in codec_weight_shapes().items():
+        n, key = int(np.prod(shape)), _tensor_seed(seed, name)
+        if "codebook" in name:
+            v = synthetic_normal(n, key, 0.0, 1.0)
+        elif ".norm." in name or "final_layer_norm" in name:
+            v = synthetic_normal(n, key, 1.0 if name.endswith("weight") else 0.0, 0.1)
+        elif name.endswith(".gamma"):
+            v = synthetic_normal(n, key, 0.5, 0.1)
+        else:
+            v = synthetic_normal(n, key, 0.0, std)
+        out[name] = v.reshape(shape)
+    return out
+
+
+class EnhancedCodec:
+    """The decode path of itts25::EnhancedCodec (include/itts25/codec.hpp:11-17) on the MI355X."""
+
+    def __init__(self, weights: Optional[Dict[str, np.ndarray]]):
+        self._c = C.c_void_p()
+        keep, tensors = [], []
+        for name, arr in (weights or {}).items():
+            a = np.ascontiguousarray(arr, dtype=np.float32)
+            keep.append(a)
+            shape = (C.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
+            tensors.append(_Tensor(name.encode(), a.ctypes.data, shape, a.ndim, 0))
+        arr_t = (_Tensor * max(1, len(tensors)))(*tensors)
+        st = _lib.itts_codec_create(arr_t, len(tensors), C.byref(self._c))
+        if st != 0:
+            _raise(st, _lib.itts_codec_last_error(None).decode())
+
+    @classmethod
+    def from_bundle(cls, bundle: "Bundle") -> "EnhancedCodec":
+        self = cls.__new__(cls)
+        self._c = C.c_void_p()
+        st = _lib.itts_codec_create_from_bundle(bundle._b, C.byref(self._c))
+        if st != 0:
+            _raise(st, _lib.itts_codec_last_error(None).decode())
+        return self
+
+    def close(self) -> None:
+        if self._c.value:
+            _lib.itts_codec_destroy(self._c)
+            self._c = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def decode(self, codes: Sequence[int]) -> np.ndarray:
+        """EnhancedCodec::decode (codec.cpp:64-72): [2T, 1024] features, time-major."""
+        ids = np.ascontiguousarray(np.asarray(codes, dtype=np.int64))
+        if ids.size and (ids.min() < 0 or ids.max() > 0xFFFFFFFF):
+            raise InvalidArgument("Codec expects 1..5000 code IDs in [0,8192)")
+        ids = ids.astype(np.uint32)
+        out = np.empty((2 * max(1, ids.size), CODEC_WIDTH), np.float32)
+        st = _lib.itts_codec_decode(self._c, _up(ids), ids.size, _fp(out))
+        if st != 0:
+            _raise(st, _lib.itts_codec_last_error(self._c).decode())
+        return out[: 2 * ids.size]
+
+    def bench(self, n: int, iters: int = 20) -> dict:
+        ms, fl = C.c_float(), C.c_double()
+        st = _lib.itts_codec_bench(self._c, int(n), int(iters), C.byref(ms), C.byref(fl))
+        if st != 0:
+            _raise(st, _lib.itts_codec_last_error(self._c).decode())
+        return {"avg_ms": float(ms.value), "flops": float(fl.value)}
 
 
 def synthetic_prefix_inputs(n_text: int, seed: int, n_cond: int = 32, text_vocab: int = 12000):

@@ -177,7 +177,7 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs)")
+    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode")
     ap.add_argument("--iters", type=int, default=240)
     ap.add_argument("--kernel-batch", type=int, default=1, help="sequences per launch for --kernel-only")
     args = ap.parse_args()
@@ -189,6 +189,12 @@ def main() -> int:
 
     weights = it.make_synthetic_weights(layers=24, seed=0)
     dec = it.GptDecoder(weights, kv_capacity=4096, max_batch=8)
+    if args.kernel_only == "codec":
+        codec = it.EnhancedCodec(it.make_synthetic_codec_weights(seed=0))
+        r = codec.bench(600, args.iters)
+        print(json.dumps({"kernel": "codec_decode", "codes": 600, "iters": args.iters, "avg_ms": round(r["avg_ms"], 4),
+                          "TFLOPs": round(r["flops"] / (r["avg_ms"] * 1e-3) / 1e12, 2)}), flush=True)
+        return 0
     if args.kernel_only:
         k = dec.bench_kernel(args.kernel_only, iters=args.iters, batch=args.kernel_batch)
         print(json.dumps({"kernel": args.kernel_only, "batch": args.kernel_batch, "iters": args.iters,

@@ -3,6 +3,7 @@
 // a device-context object, prepare -> generate.  `gpt_shim_example run` uses a synthetic
 // weight table; `gpt_shim_example bundle <dir>` loads a MIT2 bundle through itts25::BundleWeights;
 // both execute on the GPU.  Without arguments it only checks that the shim links.
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -10,6 +11,7 @@
 #include <string>
 #include <vector>
 
+#include "itts25/codec.hpp"
 #include "itts25/gpt.hpp"
 
 namespace {
@@ -149,5 +151,46 @@ int main(int argc, char** argv) {
         same = single.codes == batched[i].codes && single.stopped == batched[i].stopped;
     }
     std::printf("{\"segments\":%zu,\"segments_equal_loop\":%d}\n", batched.size(), same ? 1 : 0);
+    // The codes' consumer through the reference's construction (native_runtime.cpp:30, 100):
+    // EnhancedCodec codec_(weights_, metal_); codec_.decode(generated.codes).
+    const std::string q = "codec.quantizer.quantizers.0", d = "codec.decoder.0";
+    w.add(q + ".codebook.weight", {8192, 8}, 0, 1, seed++);
+    w.add(q + ".out_project.weight", {1024, 8}, 0, 0.02f, seed++);
+    w.add(q + ".out_project.bias", {1024}, 0, 0.02f, seed++);
+    w.add(d + ".embed.weight", {384, 1024, 7}, 0, 0.02f, seed++);
+    w.add(d + ".embed.bias", {384}, 0, 0.02f, seed++);
+    w.add(d + ".norm.weight", {384}, 1, 0.1f, seed++);
+    w.add(d + ".norm.bias", {384}, 0, 0.1f, seed++);
+    for (int i = 0; i < 12; ++i) {
+        const std::string l = d + ".convnext." + std::to_string(i);
+        w.add(l + ".dwconv.weight", {384, 1, 7}, 0, 0.02f, seed++);
+        w.add(l + ".dwconv.bias", {384}, 0, 0.02f, seed++);
+        w.add(l + ".norm.weight", {384}, 1, 0.1f, seed++);
+        w.add(l + ".norm.bias", {384}, 0, 0.1f, seed++);
+        w.add(l + ".pwconv1.weight", {2048, 384}, 0, 0.02f, seed++);
+        w.add(l + ".pwconv1.bias", {2048}, 0, 0.02f, seed++);
+        w.add(l + ".pwconv2.weight", {384, 2048}, 0, 0.02f, seed++);
+        w.add(l + ".pwconv2.bias", {384}, 0, 0.02f, seed++);
+        w.add(l + ".gamma", {384}, 0.5f, 0.1f, seed++);
+    }
+    w.add(d + ".final_layer_norm.weight", {384}, 1, 0.1f, seed++);
+    w.add(d + ".final_layer_norm.bias", {384}, 0, 0.1f, seed++);
+    w.add("codec.decoder.1.weight", {1024, 384}, 0, 0.02f, seed++);
+    w.add("codec.decoder.1.bias", {1024}, 0, 0.02f, seed++);
+    w.add("codec.up.weight", {1024, 1024, 3}, 0, 0.02f, seed++);
+    w.add("codec.up.bias", {1024}, 0, 0.02f, seed++);
+    itts25::EnhancedCodec codec(w, ctx);
+    const std::vector<uint32_t> codes = batched[0].codes.empty() ? std::vector<uint32_t>{1, 2, 3} : batched[0].codes;
+    const auto features = codec.decode(codes);
+    bool finite = true;
+    for (float v : features) finite = finite && std::isfinite(v);
+    bool refused = false;
+    try {
+        codec.decode({8192});
+    } catch (const std::invalid_argument&) {
+        refused = true;
+    }
+    std::printf("{\"codec_values\":%zu,\"codec_codes\":%zu,\"codec_finite\":%d,\"codec_refuses_8192\":%d}\n", features.size(),
+                codes.size(), finite ? 1 : 0, refused ? 1 : 0);
     return 0;
 }

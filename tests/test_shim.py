@@ -28,6 +28,9 @@ def test_shim_runs_on_gpu():
     assert lines[1]["beam_codes"] + lines[1]["beam_stopped"] >= 1
     assert lines[2]["processed"] == 8194
     assert lines[3] == {"segments": 3, "segments_equal_loop": 1}
+    c = lines[4]
+    assert c["codec_values"] == 2 * c["codec_codes"] * 1024 and c["codec_codes"] >= 1
+    assert c["codec_finite"] == 1 and c["codec_refuses_8192"] == 1
 
 
 @pytest.mark.gpu

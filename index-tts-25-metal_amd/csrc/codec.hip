@@ -24,8 +24,11 @@
 //   * codec_dwconv_ln: depthwise conv7 + LayerNorm of one 384-wide row per wave.
 //   * codec_ln: LayerNorm of one 384-wide row per wave.
 //   * codec_upsample: nearest x2 in time into the zero-padded input of the last conv.
+// A decode of a given length is captured once as a HIP graph and replayed (about 60 launches,
+// which bound short decodes); the padding rows are written by kernels, not memsets.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -62,11 +65,19 @@ __device__ __forceinline__ float codec_gelu(float x) {
     return 0.5f * x * (1.0f + erf);
 }
 
+// Row r of the embed conv's zero-padded input (T + 2 pad rows): rows pad .. pad + T - 1 are the
+// projected codebook rows of the codes, the others zero.
 __global__ __launch_bounds__(256) void codec_lookup_kernel(const uint32_t* codes, const float* cb, const float* w, const float* b,
-                                                           float* out) {
-    const int t = blockIdx.x, tid = threadIdx.x;
+                                                           float* out, int T, int pad) {
+    const int r = blockIdx.x, tid = threadIdx.x;
+    if (r < pad || r >= T + pad) {
+#pragma unroll
+        for (int i = 0; i < kCW / 256; ++i) out[static_cast<size_t>(r) * kCW + tid + 256 * i] = 0.0f;
+        return;
+    }
+    const int t = r;
     __shared__ float e[kCodeDim];
-    if (tid < kCodeDim) e[tid] = cb[static_cast<size_t>(codes[t]) * kCodeDim + tid];
+    if (tid < kCodeDim) e[tid] = cb[static_cast<size_t>(codes[r - pad]) * kCodeDim + tid];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kCW / 256; ++i) {
@@ -216,16 +227,27 @@ __global__ __launch_bounds__(256) void codec_dwconv_ln_kernel(const float* x, co
                                                               const float* gb, float* out, int T) {
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
+    // All 42 loads first (rows clamped into [0, T), taps outside it zeroed), so they are in
+    // flight together instead of one tap's branch at a time.
+    float xv[kCK][6];
+#pragma unroll
+    for (int k = 0; k < kCK; ++k) {
+        const int src = t + k - kCK / 2;
+        const int row = min(max(src, 0), T - 1);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) xv[k][i] = x[static_cast<size_t>(row) * kCH + lane + 64 * i];
+        if (src < 0 || src >= T) {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) xv[k][i] = 0.0f;
+        }
+    }
     float v[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
         const int c = lane + 64 * i;
         float acc = db[c];
 #pragma unroll
-        for (int k = 0; k < kCK; ++k) {
-            const int src = t + k - kCK / 2;
-            if (src >= 0 && src < T) acc += x[static_cast<size_t>(src) * kCH + c] * dw[c * kCK + k];
-        }
+        for (int k = 0; k < kCK; ++k) acc += xv[k][i] * dw[c * kCK + k];
         v[i] = acc;
     }
     ln384(v, gw, gb, lane);
@@ -270,13 +292,14 @@ struct Buf {
     ~Buf() {
         if (p) (void)hipFree(p);
     }
-    void ensure(size_t count) {
-        if (count <= n) return;
+    bool ensure(size_t count) {  // true when the buffer moved
+        if (count <= n) return false;
         if (p) CODEC_CHECK(hipFree(p));
         p = nullptr;
         n = 0;
         CODEC_CHECK(hipMalloc(&p, count * sizeof(T)));
         n = count;
+        return true;
     }
     void upload(const std::vector<T>& v) {
         ensure(v.size());
@@ -308,18 +331,51 @@ struct CodecEngine {
     } blk[kCBlocks];
     Buf<float> xpad, x, hn, f, y, upad, out, ws;
     Buf<uint32_t> dcodes;
+    // Decodes of one length replay a captured graph (ITTS_CODEC_GRAPHS=0: eager launches).  A
+    // buffer that moves bumps `generation`, and graphs captured before are dropped.
+    bool use_graphs = true;
+    uint64_t generation = 0, graph_generation = 0;
+    std::unordered_map<int, hipGraphExec_t> graphs;
+
+    static int used_splits(int M, int N, int K, int* kchunk) {
+        const int splits = codec_splits(M, N, K);
+        *kchunk = ((K + splits - 1) / splits + GK - 1) / GK * GK;
+        return (K + *kchunk - 1) / *kchunk;
+    }
+    static size_t ws_need(int M, int N, int K) {
+        int kc = 0;
+        const int used = used_splits(M, N, K, &kc);
+        return used > 1 ? static_cast<size_t>(used) * M * N : 0;
+    }
+    template <class B>
+    void grow(B& b, size_t n) {
+        if (b.ensure(n)) ++generation;
+    }
+    // Every buffer a decode of T codes touches, sized before anything is queued (and captured).
+    void reserve(int T) {
+        const size_t pad = kCK / 2;
+        grow(dcodes, T);
+        grow(xpad, (T + 2 * pad) * kCW);
+        grow(x, static_cast<size_t>(T) * kCH);
+        grow(hn, static_cast<size_t>(T) * kCH);
+        grow(f, static_cast<size_t>(T) * kCF);
+        grow(y, static_cast<size_t>(T) * kCW);
+        grow(upad, static_cast<size_t>(2 * T + 2) * kCW);
+        grow(out, static_cast<size_t>(2 * T) * kCW);
+        size_t w = std::max({ws_need(T, kCH, kCK * kCW), ws_need(T, kCF, kCH), ws_need(T, kCH, kCF), ws_need(T, kCW, kCH),
+                             ws_need(2 * T, kCW, kUpK * kCW)});
+        grow(ws, std::max<size_t>(w, 1));
+    }
 
     template <int EPI>
     void gemm(CodecGemm g) {
         if (g.N % GN || g.K % GK || g.M < 1) throw std::logic_error("codec GEMM shape");
-        const int splits = codec_splits(g.M, g.N, g.K);
-        g.kchunk = ((g.K + splits - 1) / splits + GK - 1) / GK * GK;
-        const int used = (g.K + g.kchunk - 1) / g.kchunk;
+        const int used = used_splits(g.M, g.N, g.K, &g.kchunk);
         const dim3 grid(g.N / GN, (g.M + GM - 1) / GM, used);
         if (used == 1) {
             hipLaunchKernelGGL((codec_gemm_kernel<EPI, false>), grid, dim3(256), 0, stream, g);
         } else {
-            ws.ensure(static_cast<size_t>(used) * g.M * g.N);
+            if (ws.n < static_cast<size_t>(used) * g.M * g.N) throw std::logic_error("codec split-K workspace not reserved");
             g.ws = ws.p;
             hipLaunchKernelGGL((codec_gemm_kernel<EPI, true>), grid, dim3(256), 0, stream, g);
             CODEC_CHECK(hipGetLastError());
@@ -331,6 +387,7 @@ struct CodecEngine {
     std::string last_error;
 
     ~CodecEngine() {
+        drop_graphs();
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
         if (stream) (void)hipStreamDestroy(stream);
@@ -382,6 +439,8 @@ struct CodecEngine {
         dec_b.upload(vec(get("codec.decoder.1.bias", {kCW}), kCW));
         up_w.upload(conv_w(get("codec.up.weight", {kCW, kCW, kUpK}), kCW, kCW, kUpK));
         up_b.upload(vec(get("codec.up.bias", {kCW}), kCW));
+        const char* env = std::getenv("ITTS_CODEC_GRAPHS");
+        use_graphs = !(env && std::strcmp(env, "0") == 0);
         CODEC_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         for (auto& e : ev) CODEC_CHECK(hipEventCreate(&e));
     }
@@ -392,21 +451,12 @@ struct CodecEngine {
         if (!ok) throw std::invalid_argument("Codec expects 1..5000 code IDs in [0,8192)");
     }
 
-    // The whole decode of T codes already in dcodes, queued on the stream; result in out.
+    // The whole decode of T codes already in dcodes, queued on the stream (kernels only, into
+    // buffers reserve(T) sized); result in out.
     void enqueue(int T) {
-        const size_t pad = kCK / 2;
-        xpad.ensure((T + 2 * pad) * kCW);
-        x.ensure(static_cast<size_t>(T) * kCH);
-        hn.ensure(static_cast<size_t>(T) * kCH);
-        f.ensure(static_cast<size_t>(T) * kCF);
-        y.ensure(static_cast<size_t>(T) * kCW);
-        upad.ensure(static_cast<size_t>(2 * T + 2) * kCW);
-        out.ensure(static_cast<size_t>(2 * T) * kCW);
+        const int pad = kCK / 2;
         hipStream_t s = stream;
-        // padding rows of the embed conv's input: the lookup writes rows 3 .. T + 2
-        CODEC_CHECK(hipMemsetAsync(xpad.p, 0, pad * kCW * 4, s));
-        CODEC_CHECK(hipMemsetAsync(xpad.p + (T + pad) * kCW, 0, pad * kCW * 4, s));
-        hipLaunchKernelGGL(codec_lookup_kernel, dim3(T), dim3(256), 0, s, dcodes.p, cb.p, op_w.p, op_b.p, xpad.p + pad * kCW);
+        hipLaunchKernelGGL(codec_lookup_kernel, dim3(T + 2 * pad), dim3(256), 0, s, dcodes.p, cb.p, op_w.p, op_b.p, xpad.p, T, pad);
         CODEC_CHECK(hipGetLastError());
         const int rows4 = (T + 3) / 4;
         gemm<kEpiBias>({xpad.p, kCW, emb_w.p, emb_b.p, nullptr, x.p, kCH, T, kCH, kCK * kCW, nullptr, 0});
@@ -427,11 +477,46 @@ struct CodecEngine {
         gemm<kEpiBias>({upad.p, kCW, up_w.p, up_b.p, nullptr, out.p, kCW, 2 * T, kCW, kUpK * kCW, nullptr, 0});
     }
 
+    void drop_graphs() {
+        for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+        graphs.clear();
+    }
+    // One decode of T codes: a replay of its captured graph, or eager launches.
+    void run(int T) {
+        if (!use_graphs) {
+            enqueue(T);
+            return;
+        }
+        if (graph_generation != generation || graphs.size() >= 64) {
+            drop_graphs();
+            graph_generation = generation;
+        }
+        auto it = graphs.find(T);
+        if (it == graphs.end()) {
+            hipGraph_t g = nullptr;
+            CODEC_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+            try {
+                enqueue(T);
+            } catch (...) {
+                (void)hipStreamEndCapture(stream, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            CODEC_CHECK(hipStreamEndCapture(stream, &g));
+            hipGraphExec_t exec = nullptr;
+            const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            CODEC_CHECK(e);
+            it = graphs.emplace(T, exec).first;
+        }
+        CODEC_CHECK(hipGraphLaunch(it->second, stream));
+    }
+
     void decode(const uint32_t* codes, uint32_t n, float* host_out) {
         check_codes(codes, n);
-        dcodes.ensure(n);
+        reserve(static_cast<int>(n));
         CODEC_CHECK(hipMemcpyAsync(dcodes.p, codes, n * 4, hipMemcpyHostToDevice, stream));
-        enqueue(static_cast<int>(n));
+        run(static_cast<int>(n));
         CODEC_CHECK(hipMemcpyAsync(host_out, out.p, static_cast<size_t>(2) * n * kCW * 4, hipMemcpyDeviceToHost, stream));
         CODEC_CHECK(hipStreamSynchronize(stream));
     }
@@ -442,11 +527,11 @@ struct CodecEngine {
         if (!iters || n < 1 || n > static_cast<uint32_t>(kMaxCodes)) throw std::invalid_argument("Invalid codec benchmark request");
         std::vector<uint32_t> codes(n);
         for (uint32_t i = 0; i < n; ++i) codes[i] = (i * 2654435761u) % kCodebook;
-        dcodes.ensure(n);
+        reserve(static_cast<int>(n));
         CODEC_CHECK(hipMemcpyAsync(dcodes.p, codes.data(), n * 4, hipMemcpyHostToDevice, stream));
-        enqueue(static_cast<int>(n));  // warm-up (and buffer sizing)
+        run(static_cast<int>(n));  // warm-up (and the graph's capture)
         CODEC_CHECK(hipEventRecord(ev[0], stream));
-        for (uint32_t i = 0; i < iters; ++i) enqueue(static_cast<int>(n));
+        for (uint32_t i = 0; i < iters; ++i) run(static_cast<int>(n));
         CODEC_CHECK(hipEventRecord(ev[1], stream));
         CODEC_CHECK(hipEventSynchronize(ev[1]));
         float ms = 0;

@@ -109,6 +109,26 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     for (int i = t; i < V; i += NT) out[i] = sm.s[i] + score;
 }
 
+// Calls f(i, src[i]) for i = first, first + step, ... < end, in that order, with the loads of
+// eight consecutive visits in flight together: a loop that waits for each global load before
+// the next pays one memory round trip per element.
+template <class F>
+__device__ __forceinline__ void for_each_batched(const float* src, int first, int end, int step, F f) {
+    for (int base = first; base < end; base += 8 * step) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = base + u * step;
+            x[u] = i < end ? src[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = base + u * step;
+            if (i < end) f(i, x[u]);
+        }
+    }
+}
+
 // kk-th largest (1-based) of src[0..n) in global memory.
 __device__ float radix_kth_largest_global(const float* src, int n, uint32_t kk, uint32_t* hist, uint32_t* sel) {
     const int t = threadIdx.x, lane = t & 63;
@@ -116,10 +136,10 @@ __device__ float radix_kth_largest_global(const float* src, int n, uint32_t kk, 
     for (int shift = 24; shift >= 0; shift -= 8) {
         if (t < 256) hist[t] = 0;
         __syncthreads();
-        for (int i = t; i < n; i += NT) {
-            const uint32_t k = float_key(src[i]);
+        for_each_batched(src, t, n, NT, [&](int, float v) {
+            const uint32_t k = float_key(v);
             if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-        }
+        });
         __syncthreads();
         if (t < 64) {
             uint32_t c[4];
@@ -248,21 +268,21 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     if (!a.do_sample) {
         const float pivot = radix_kth_largest_global(S, n, static_cast<uint32_t>(take), hist, sel);
         uint32_t cg = 0, ce = 0;
-        for (int i = i0; i < i1; ++i) {
-            cg += S[i] > pivot;
-            ce += S[i] == pivot;
-        }
+        for_each_batched(S, i0, i1, 1, [&](int, float v) {
+            cg += v > pivot;
+            ce += v == pivot;
+        });
         uint32_t ng = 0, ne = 0;
         uint32_t og = block_scan(cg, wtot, &ng);
         uint32_t oe = block_scan(ce, wtot, &ne);
         const uint32_t need = static_cast<uint32_t>(take) - ng;  // ties at the pivot, smallest indices first
-        for (int i = i0; i < i1; ++i) {
-            if (S[i] > pivot) ids[og++] = static_cast<uint32_t>(i);
-            else if (S[i] == pivot) {
+        for_each_batched(S, i0, i1, 1, [&](int i, float v) {
+            if (v > pivot) ids[og++] = static_cast<uint32_t>(i);
+            else if (v == pivot) {
                 if (oe < need) ids[ng + oe] = static_cast<uint32_t>(i);
                 ++oe;
             }
-        }
+        });
         __syncthreads();
         if (t == 0) {
             // (score desc, index asc): the order std::partial_sort produces with index ties.
@@ -280,18 +300,17 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     } else {
         // Finite entries in index order, kept in global scratch (a.list), weights in a.probs.
         uint32_t c = 0;
-        for (int i = i0; i < i1; ++i) c += finite_f(S[i]);
+        for_each_batched(S, i0, i1, 1, [&](int, float v) { c += finite_f(v); });
         uint32_t F = 0;
         uint32_t off = block_scan(c, wtot, &F);
         if (F <= static_cast<uint32_t>(kLdsCands)) {
-            for (int i = i0; i < i1; ++i) {
-                const float v = S[i];
+            for_each_batched(S, i0, i1, 1, [&](int i, float v) {
                 if (finite_f(v)) {
                     lid[off] = static_cast<uint32_t>(i);
                     lsc[off] = v;
                     ++off;
                 }
-            }
+            });
             __syncthreads();
             if (wave != 0) return;
             uint64_t rng = *a.rng;
@@ -320,8 +339,9 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
             }
             return;
         }
-        for (int i = i0; i < i1; ++i)
-            if (finite_f(S[i])) a.list[off++] = static_cast<uint32_t>(i);
+        for_each_batched(S, i0, i1, 1, [&](int i, float v) {
+            if (finite_f(v)) a.list[off++] = static_cast<uint32_t>(i);
+        });
         __syncthreads();
         if (t == 0) stop_s = 0;
         uint64_t rng = *a.rng;

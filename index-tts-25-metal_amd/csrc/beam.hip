@@ -61,31 +61,32 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     for (int i = t; i < V; i += NT) e[i] = expf_cr(sm.s[i] - peak);
     __syncthreads();
     if (t == 0) {
-        // sum += e[0], e[1], ... in index order; the next 16 values are read while the
-        // current 16 are added
+        // sum += e[0], e[1], ... in index order; the next 32 values are read while the
+        // current 32 are added
         constexpr int kQuads = V / 4;  // 2048: 8192 values, then the last V % 4
-        static_assert(kQuads % 8 == 0, "two chunks of four quads per iteration");
+        constexpr int kQ = 8;          // quads per register chunk
+        static_assert(kQuads % (2 * kQ) == 0, "two chunks of kQ quads per iteration");
         const float4* e4 = reinterpret_cast<const float4*>(e);
         float sum = 0.0f;
-        float4 c0[4], c1[4];
+        float4 c0[kQ], c1[kQ];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) c0[k] = e4[k];
-        for (int q0 = 0; q0 < kQuads; q0 += 8) {
+        for (int k = 0; k < kQ; ++k) c0[k] = e4[k];
+        for (int q0 = 0; q0 < kQuads; q0 += 2 * kQ) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) c1[k] = e4[q0 + 4 + k];
+            for (int k = 0; k < kQ; ++k) c1[k] = e4[q0 + kQ + k];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < kQ; ++k) {
                 sum += c0[k].x;
                 sum += c0[k].y;
                 sum += c0[k].z;
                 sum += c0[k].w;
             }
-            if (q0 + 8 < kQuads) {
+            if (q0 + 2 * kQ < kQuads) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) c0[k] = e4[q0 + 8 + k];
+                for (int k = 0; k < kQ; ++k) c0[k] = e4[q0 + 2 * kQ + k];
             }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < kQ; ++k) {
                 sum += c1[k].x;
                 sum += c1[k].y;
                 sum += c1[k].z;
@@ -216,10 +217,22 @@ __device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, uint32
             if (!(lid[j] & kTaken)) m = fmaxf(m, lsc[j]);
         m = wave_max(m);
         if (m == -INFINITY) return kNoFinite;
+        // Up to 128 candidates: each weight is evaluated once per draw (registers pa, pb) and
+        // used by both passes below; more candidates are re-evaluated in the second pass.
+        const bool small = F <= 128;
+        double pa = 0.0, pb = 0.0;
+        if (small) {
+            if (lane < F && !(lid[lane] & kTaken)) pa = exp(static_cast<double>(lsc[lane] - m));
+            if (64 + lane < F && !(lid[64 + lane] & kTaken)) pb = exp(static_cast<double>(lsc[64 + lane] - m));
+        }
+        auto weight = [&](uint32_t c0) -> double {
+            if (small) return c0 == 0 ? pa : pb;
+            const uint32_t j = c0 + lane;
+            return j < F && !(lid[j] & kTaken) ? exp(static_cast<double>(lsc[j] - m)) : 0.0;
+        };
         double total = 0.0;
         for (uint32_t c0 = 0; c0 < F; c0 += 64) {
-            const uint32_t j = c0 + lane;
-            const double p = j < F && !(lid[j] & kTaken) ? exp(static_cast<double>(lsc[j] - m)) : 0.0;
+            const double p = weight(c0);
             const int cn = static_cast<int>(min(64u, F - c0));
             for (int q = 0; q < cn; ++q) total += readlane_f64(p, q);
         }
@@ -228,8 +241,7 @@ __device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, uint32
         double cumulative = 0.0;
         uint32_t pick = 0xffffffffu, last = 0xffffffffu;
         for (uint32_t c0 = 0; c0 < F && pick == 0xffffffffu; c0 += 64) {
-            const uint32_t j = c0 + lane;
-            const double p = j < F && !(lid[j] & kTaken) ? exp(static_cast<double>(lsc[j] - m)) : 0.0;
+            const double p = weight(c0);
             const int cn = static_cast<int>(min(64u, F - c0));
             for (int q = 0; q < cn; ++q) {
                 const double pq = readlane_f64(p, q);

@@ -200,10 +200,11 @@ struct Engine {
     std::string last_error;
 
     ~Engine() {
-        if (step_ok) {
-            if (stream) (void)hipStreamSynchronize(stream);  // no grid of this decoder outlives its registration
-            unregister_step_user(step_dev);
-        }
+        // Queued work may still write this handle's buffers (a beam search that raised with
+        // later steps in flight copies into the pinned ring), and no persistent grid of this
+        // decoder may outlive its registration: drain the stream before anything is freed.
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (step_ok) unregister_step_user(step_dev);
         for (auto& kvp : graphs) (void)hipGraphExecDestroy(kvp.second);
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);

@@ -526,3 +526,24 @@ def test_decoder_from_bundle_bitwise_equals_arrays(itts, small_weights, tmp_path
         assert list(ra.codes) == list(rd.codes) and ra.stopped == rd.stopped
         a.close()
         d.close()
+
+
+def test_beam_error_with_queued_steps(itts, small_weights):
+    """A beam search that raises (its best candidate is code 8192, gpt_sampling.cpp:234) while
+    later steps are already queued: the queued steps stay in bounds (all children inactive),
+    the decoder closes cleanly, and a new search works."""
+    w = dict(small_weights)
+    hb = w["gpt.mel_head.bias"].copy()
+    hb[8192] += 6.0
+    w["gpt.mel_head.bias"] = hb
+    dec = itts.GptDecoder(w, kv_capacity=1024, max_batch=4)
+    cond, text = itts.synthetic_prefix_inputs(20, seed=4)
+    prefix = dec.prepare_cond(cond, text, 0)
+    with pytest.raises(itts.GptRuntimeError, match="Beam generated invalid semantic code"):
+        # penalty 1: 8192 is in every history ({1, 8192}, gpt_sampling.cpp:176), which a penalty would push down
+        dec.generate(prefix, itts.GenerationOptions(do_sample=False, num_beams=3, repetition_penalty=1.0), 32)
+    dec.close()
+    ok = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=4)
+    r = ok.generate(ok.prepare_cond(cond, text, 0), itts.GenerationOptions(num_beams=3, seed=1, suppress_stop=True), 8)
+    assert len(r.codes) == 8
+    ok.close()

@@ -177,7 +177,7 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode")
+    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode; 'beam3': the beam-3 workload")
     ap.add_argument("--iters", type=int, default=240)
     ap.add_argument("--kernel-batch", type=int, default=1, help="sequences per launch for --kernel-only")
     args = ap.parse_args()
@@ -189,6 +189,18 @@ def main() -> int:
 
     weights = it.make_synthetic_weights(layers=24, seed=0)
     dec = it.GptDecoder(weights, kv_capacity=4096, max_batch=8)
+    if args.kernel_only == "beam3":
+        # the extras' beam-3 workload alone: 32 latents + 80 text ids, 3 beams, 400 codes
+        cond, text = it.synthetic_prefix_inputs(80, seed=3)
+        prefix = dec.prepare_cond(cond, text, 0)
+        o = it.GenerationOptions(num_beams=3, length_penalty=0.0, repetition_penalty=10.0, seed=7, suppress_stop=True)
+        dec.generate(prefix, o, 32)
+        r = dec.generate(prefix, o, 400)
+        tm = dec.last_timing()
+        print(json.dumps({"kernel": "beam3", "codes": len(r.codes), "beam_steps": tm["decode_steps"],
+                          "beam_tokens_per_s": round(3 * tm["decode_steps"] / (tm["decode_ms"] * 1e-3), 2),
+                          "ms_per_beam_step": round(tm["decode_ms"] / tm["decode_steps"], 4)}), flush=True)
+        return 0
     if args.kernel_only == "codec":
         codec = it.EnhancedCodec(it.make_synthetic_codec_weights(seed=0))
         r = codec.bench(600, args.iters)

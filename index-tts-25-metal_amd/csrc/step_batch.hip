@@ -478,8 +478,8 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             // 1280-float rows (raw and normalised h) that c_attn reads, so it may be written
             // while other waves still run c_attn.
             float* qwin = &sm.stage[0][2 * kWidth];
-            // One tile's rows in registers: the next round's K is issued once this round's
-            // scores are formed, its V once this round's weighted sum is.
+            // One tile's rows in registers: the next tile round's K is issued once this tile
+            // round's scores are formed, its V once its weighted sum is.
             uint32_t off[4];
             float4 kk[4], vv[4];
             tile_rows<B>(a, P, 0, kvl, g, sub, off);

@@ -1,6 +1,6 @@
 """CPU restatement of EnhancedCodec::decode (src/codec.cpp:57-72) in float64 numpy.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of the HIP codec decode.
+TEST INFRASTRUCTURE ONLY: imported by tests/, which compare the HIP codec decode against it.
 
 Each function follows the reference op it names:
   * lookup           codec.cpp:57-63: codebook rows (mit2_embedding_f32, kernels.metal:281-294),

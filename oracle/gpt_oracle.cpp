@@ -1,7 +1,8 @@
 // CPU oracle for the IndexTTS 2.5 GPT semantic-token loop.
 //
 // TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's CPU
-// baseline leg load this library as the checker.  The product never links it.
+// baseline leg load this library to compare the HIP path against.  The product never
+// links it.
 //
 // Follows, op for op:
 //   src/gpt.cpp:42-71    prefix construction (prepare)

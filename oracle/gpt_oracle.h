@@ -2,8 +2,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain FP32 C++ restatement of the
  * reference op sequence (src/gpt.cpp:42-125) and of its sampler / generation
- * loop (src/gpt_sampling.cpp:11-245).  It is the checker that the HIP path is
- * compared against and the timed CPU baseline; nothing in the product links it.
+ * loop (src/gpt_sampling.cpp:11-245).  The HIP path is compared against it, and it is
+ * the timed CPU baseline; nothing in the product links it.
  *
  * Pinning (what checks each function, other than retyping it):
  *   orc_splitmix_*        published SplitMix64 test vectors; the reference's own

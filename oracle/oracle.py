@@ -2,8 +2,8 @@
 sampler compiled from its sources (oracle/_ref/ref_sampling).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the CPU
-baseline leg of bench.py, as the checker.  See gpt_oracle.h for what each function
-restates and what pins it.
+baseline leg of bench.py, which compare the HIP path against it.  See gpt_oracle.h for
+what each function restates and what pins it.
 """
 from __future__ import annotations
 

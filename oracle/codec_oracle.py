@@ -19,8 +19,9 @@ What pins each one (tests/test_codec_oracle.py): conv kernels that are a unit im
 j shift the input by j - pad (identity at j = pad) and a brute-force loop over the Metal
 kernel's index arithmetic on tiny shapes; LayerNorm rows have zero mean and unit variance;
 the GELU's erf is within the published 1.5e-7 bound of math.erf on a dense grid (a wrong
-coefficient breaks the bound); the upsampling equals np.repeat(x, 2); decode's composition
-equals a step-by-step evaluation on a tiny model.
+coefficient breaks the bound); the upsampling equals np.repeat(x, 2).  vocos() and decode()
+only compose those pieces in codec.cpp's order (36-48, 64-72); no check of their own pins the
+composition beyond its pinned parts (its agreement with the HIP decode is parity, not a pin).
 """
 from __future__ import annotations
 

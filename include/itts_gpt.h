@@ -230,6 +230,16 @@ int itts_codec_decode(itts_codec* c, const uint32_t* codes, uint32_t n, float* o
  * decode of n codes over `iters` back-to-back runs (HIP events), and its GEMM FLOPs. */
 int itts_codec_bench(itts_codec* c, uint32_t n, uint32_t iters, float* avg_ms, double* flops);
 
+/* Verification hook (no reference counterpart): the device expf / exp / logf that the
+ * sampler and beam kernels use in place of the reference's libm calls
+ * (gpt_sampling.cpp:96, :144, :207-210), evaluated on the float inputs whose bit patterns
+ * are first_bits + i * stride, i < count (<= 2^28).  ITTS_LIBM_EXP takes each float widened
+ * to double and writes doubles; the others write floats.  out is host memory. */
+#define ITTS_LIBM_EXPF 0
+#define ITTS_LIBM_EXP 1
+#define ITTS_LIBM_LOGF 2
+int itts_libm_eval(int32_t fn, uint64_t first_bits, uint64_t stride, uint64_t count, void* out);
+
 /* Deterministic N(mean, std^2) fill for synthetic weights and inputs: value i is
  * a Box-Muller transform of two SplitMix64 outputs keyed by (seed, i), so the
  * result does not depend on thread count.  Host only. */

@@ -3,8 +3,7 @@
 // beam_scores_kernel, one 1024-thread workgroup per parent beam:
 //   log_probs = logits - (peak + log(sum_i exp(logit_i - peak)))   (:207-210, float; the
 //   sum is formed by one lane in index order from 16-byte LDS reads issued a chunk ahead,
-//   exp/log evaluated in double and rounded, i.e. correctly rounded except on
-//   double-rounding ties), then the processors with the
+//   expf/logf bit for bit those of glibc (glibc_math.h)), then the processors with the
 //   parent's repetition set (:211-212), then + the parent's beam score (:213).
 // beam_select_kernel, one workgroup:
 //   greedy: the take = 2*beams best of all parents' scores by (score desc, index asc)
@@ -21,8 +20,6 @@ namespace itts {
 namespace {
 using namespace sampling;
 
-__device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
-__device__ __forceinline__ float logf_cr(float x) { return static_cast<float>(log(static_cast<double>(x))); }
 
 __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     __shared__ Smem sm;
@@ -58,7 +55,7 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     __syncthreads();
     float peak = wred[0];
     for (int w = 1; w < NWAVE; ++w) peak = fmaxf(peak, wred[w]);
-    for (int i = t; i < V; i += NT) e[i] = expf_cr(sm.s[i] - peak);
+    for (int i = t; i < V; i += NT) e[i] = libm::expf_glibc(sm.s[i] - peak);
     __syncthreads();
     if (t == 0) {
         // sum += e[0], e[1], ... in index order; the next 32 values are read while the
@@ -94,7 +91,7 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
             }
         }
         for (int i = kQuads * 4; i < V; ++i) sum += e[i];
-        log_sum_s = peak + logf_cr(sum);
+        log_sum_s = peak + libm::logf_glibc(sum);
     }
     __syncthreads();
     const float log_sum = log_sum_s;
@@ -222,13 +219,13 @@ __device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, uint32
         const bool small = F <= 128;
         double pa = 0.0, pb = 0.0;
         if (small) {
-            if (lane < F && !(lid[lane] & kTaken)) pa = exp(static_cast<double>(lsc[lane] - m));
-            if (64 + lane < F && !(lid[64 + lane] & kTaken)) pb = exp(static_cast<double>(lsc[64 + lane] - m));
+            if (lane < F && !(lid[lane] & kTaken)) pa = libm::exp_glibc(static_cast<double>(lsc[lane] - m));
+            if (64 + lane < F && !(lid[64 + lane] & kTaken)) pb = libm::exp_glibc(static_cast<double>(lsc[64 + lane] - m));
         }
         auto weight = [&](uint32_t c0) -> double {
             if (small) return c0 == 0 ? pa : pb;
             const uint32_t j = c0 + lane;
-            return j < F && !(lid[j] & kTaken) ? exp(static_cast<double>(lsc[j] - m)) : 0.0;
+            return j < F && !(lid[j] & kTaken) ? libm::exp_glibc(static_cast<double>(lsc[j] - m)) : 0.0;
         };
         double total = 0.0;
         for (uint32_t c0 = 0; c0 < F; c0 += 64) {
@@ -379,7 +376,7 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
             }
             for (uint32_t j = t; j < F; j += NT) {
                 const uint32_t id = a.list[j];
-                a.probs[j] = (id & 0x80000000u) ? 0.0 : exp(static_cast<double>(S[id] - mx));
+                a.probs[j] = (id & 0x80000000u) ? 0.0 : libm::exp_glibc(static_cast<double>(S[id] - mx));
             }
             __syncthreads();
             if (t == 0) {

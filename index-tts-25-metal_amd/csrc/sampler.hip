@@ -51,7 +51,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SampleArgs a) {
                 else {
                     double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : Pg;
                     const float mx = sm.mx;
-                    for (uint32_t j = t; j < m; j += NT) P[j] = exp(static_cast<double>(sm.s[sm.list[j]] - mx));
+                    for (uint32_t j = t; j < m; j += NT) P[j] = libm::exp_glibc(static_cast<double>(sm.s[sm.list[j]] - mx));
                     __syncthreads();
                 }
             }

@@ -18,6 +18,7 @@
 // loads 64 terms at a time into its lanes and lane-serial code reads them back with
 // v_readlane, so the chain of adds waits on no LDS round trip.
 #pragma once
+#include "glibc_math.h"
 #include "kernels.h"
 
 namespace itts {
@@ -305,7 +306,7 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
     if (m == 0) return kTopPEmpty;
     const float mx = sm.mx;
     double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : P_global;
-    for (uint32_t j = t; j < m; j += NT) P[j] = exp(static_cast<double>(sm.s[sm.list[j]] - mx));
+    for (uint32_t j = t; j < m; j += NT) P[j] = libm::exp_glibc(static_cast<double>(sm.s[sm.list[j]] - mx));
     // Keys: (score key << 32) | j; j increases with the index, so ties break by index.
     int n = 64;
     while (n < static_cast<int>(m)) n <<= 1;

@@ -119,6 +119,7 @@ def _load() -> C.CDLL:
         "itts_codec_last_error": (C.c_char_p, [P]),
         "itts_codec_decode": (C.c_int, [P, u32p, u32, f32p]),
         "itts_codec_bench": (C.c_int, [P, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
+        "itts_libm_eval": (C.c_int, [i32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_void_p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -385,7 +385,7 @@ GenResult generate_beams(orc_model& m, const std::vector<float>& prefix, const o
     for (uint32_t i = 1; i < beams.size(); ++i) beams[i].score = -1e9f;
     auto finish = [&](const Beam& beam, float score, uint32_t length, bool eos) {
         finished.push_back({beam.codes, score / std::pow(static_cast<double>(std::max(length, 1u)), config.length_penalty), eos});
-        // <= num_beams + 1 entries: libstdc++'s std::sort is an insertion sort there (stable).
+        // <= num_beams + 1 <= 11 entries: libc++'s std::sort keeps equal elements in order there.
         std::stable_sort(finished.begin(), finished.end(), [](const auto& a, const auto& b) { return a.score > b.score; });
         if (finished.size() > config.num_beams) finished.resize(config.num_beams);
     };
@@ -423,8 +423,10 @@ GenResult generate_beams(orc_model& m, const std::vector<float>& prefix, const o
                 candidates.push_back({id / kMelVocab, id % kMelVocab, all_scores[id]});
             }
         }
-        // The reference uses std::sort here; for take <= 16 libstdc++'s std::sort is an
-        // insertion sort, i.e. stable.  stable_sort keeps that order for every size.
+        // The reference uses std::sort here, built with AppleClang 17 / libc++
+        // (docs/standalone-build.txt:1), whose std::sort sorts fewer than 24 elements with
+        // stable sorting networks (2..5) and an insertion sort: for take = 2*num_beams <= 20
+        // that is the stable order.
         std::stable_sort(candidates.begin(), candidates.end(), [](const auto& a, const auto& b) { return a.score > b.score; });
         std::vector<Beam> next;
         for (uint32_t rank = 0; rank < candidates.size(); ++rank) {
@@ -681,6 +683,28 @@ int orc_kv_row(const orc_model* m, uint32_t layer, int32_t is_v, uint32_t pos, f
     });
 }
 
+struct orc_state {
+    std::shared_ptr<Snapshot> s;
+};
+
+orc_state* orc_checkpoint(const orc_model* m) {
+    orc_state* out = nullptr;
+    (void)guarded([&] {
+        if (!m->cached) throw std::invalid_argument("Invalid KV snapshot");
+        out = new orc_state{checkpoint(*m)};
+    });
+    return out;
+}
+
+int orc_restore(orc_model* m, const orc_state* st) {
+    return guarded([&] {
+        if (!st || !st->s || !st->s->tokens) throw std::invalid_argument("Invalid KV restore");
+        restore(*m, *st->s);
+    });
+}
+
+void orc_state_free(orc_state* st) { delete st; }
+
 int orc_processors(const float* logits, uint32_t vocab, const uint32_t* history, uint32_t n_history,
                    const orc_options* opt, float* out) {
     return guarded([&] {
@@ -722,6 +746,21 @@ int orc_generate(orc_model* m, const float* prefix, uint32_t rows, const orc_opt
         *n_codes = static_cast<uint32_t>(r.codes.size());
         *stopped = r.stopped ? 1 : 0;
     });
+}
+
+void orc_libm_eval(int32_t fn, uint64_t first, uint64_t stride, uint64_t count, void* out) {
+#pragma omp parallel for schedule(static)
+    for (uint64_t i = 0; i < count; ++i) {
+        const uint32_t b = static_cast<uint32_t>(first + i * stride);
+        float x;
+        std::memcpy(&x, &b, 4);
+        if (fn == 0)
+            static_cast<float*>(out)[i] = expf(x);
+        else if (fn == 1)
+            static_cast<double*>(out)[i] = exp(static_cast<double>(x));
+        else
+            static_cast<float*>(out)[i] = logf(x);
+    }
 }
 
 float orc_gelu(float v) { return gelu(v); }

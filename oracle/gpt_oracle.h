@@ -17,8 +17,10 @@
  *   orc_prepare_*         exact gather-and-add identities.
  *   orc_generate          greedy reduces to argmax of teacher-forced logits;
  *                         sampled path == processors + sample per step (_ref).
- *   orc_generate_beams    parity unpinned beyond properties: the reference's
- *                         generate_beams needs its Metal decoder to link.
+ *   orc_generate (beams)  exhaustive search on a bias-only head, where beam search
+ *                         must return the best hypothesis (tests/beam_brute.py), and a
+ *                         hand-derived case for the -1e9 initial beam scores
+ *                         (tests/test_beam_oracle.py).
  */
 #pragma once
 #include <stddef.h>
@@ -73,6 +75,11 @@ int orc_prepare_cond(orc_model* m, const float* cond, uint32_t n_cond, const uin
 /* gpt.cpp:72-85: prefill resets the cache; step appends one row. */
 int orc_prefill(orc_model* m, const float* prefix, uint32_t rows, float* logits);
 int orc_step(orc_model* m, uint32_t code, uint32_t position, float* logits);
+/* gpt.cpp:86-87: a copy of the cached K/V rows, and its restore (NULL on error). */
+typedef struct orc_state orc_state;
+orc_state* orc_checkpoint(const orc_model* m);
+int orc_restore(orc_model* m, const orc_state* st);
+void orc_state_free(orc_state* st);
 /* Read back the K or V row `pos` of layer `layer` (width floats). */
 int orc_kv_row(const orc_model* m, uint32_t layer, int32_t is_v, uint32_t pos, float* out);
 
@@ -86,6 +93,11 @@ double orc_splitmix_unit(uint64_t* state);
 /* gpt_sampling.cpp:168-245.  codes_out holds max_tokens entries. */
 int orc_generate(orc_model* m, const float* prefix, uint32_t rows, const orc_options* opt, uint32_t max_tokens,
                  uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped);
+
+/* The C library's expf(x) (fn 0), exp((double)x) (fn 1) or logf(x) (fn 2) on the float
+ * inputs with bit patterns first + i * stride, i < count: the libm calls of
+ * gpt_sampling.cpp:96, :144, :207-210, for comparison with the device's. */
+void orc_libm_eval(int32_t fn, uint64_t first, uint64_t stride, uint64_t count, void* out);
 
 /* Elementwise pieces exposed for kernel-level tests. */
 float orc_gelu(float v);

@@ -53,12 +53,16 @@ def _load() -> C.CDLL:
         "orc_prefill": (C.c_int, [P, f32p, u32, f32p]),
         "orc_step": (C.c_int, [P, u32, u32, f32p]),
         "orc_kv_row": (C.c_int, [P, u32, C.c_int32, u32, f32p]),
+        "orc_checkpoint": (P, [P]),
+        "orc_restore": (C.c_int, [P, P]),
+        "orc_state_free": (None, [P]),
         "orc_processors": (C.c_int, [f32p, u32, u32p, u32, C.POINTER(_O), f32p]),
         "orc_sample": (C.c_int, [f32p, u32, C.POINTER(C.c_uint64), u32p]),
         "orc_splitmix_next": (C.c_uint64, [C.POINTER(C.c_uint64)]),
         "orc_splitmix_unit": (C.c_double, [C.POINTER(C.c_uint64)]),
         "orc_generate": (C.c_int, [P, f32p, u32, C.POINTER(_O), u32, u32p, u32p, C.POINTER(C.c_int32)]),
         "orc_gelu": (C.c_float, [C.c_float]),
+        "orc_libm_eval": (None, [C.c_int32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_void_p]),
         "orc_layernorm": (None, [f32p, f32p, f32p, u32, C.c_float, f32p]),
         "orc_last_error": (C.c_char_p, []),
     }
@@ -101,6 +105,18 @@ def options_from(o) -> _O:
     """Convert an itts_gpt.GenerationOptions (same fields) to the oracle struct."""
     return options(o.do_sample, o.seed, o.temperature, o.top_k, o.top_p, o.repetition_penalty, o.num_beams,
                    o.length_penalty, o.suppress_stop)
+
+
+class OracleState:
+    """A KV snapshot (gpt.cpp:86-87) of an OracleGpt."""
+
+    def __init__(self, h):
+        self._h = h
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            _lib.orc_state_free(self._h)
+            self._h = None
 
 
 class OracleGpt:
@@ -153,6 +169,15 @@ class OracleGpt:
         _check(_lib.orc_step(self._h, int(code) & 0xFFFFFFFF, int(position) & 0xFFFFFFFF, _fp(out)))
         return out
 
+    def checkpoint(self) -> "OracleState":
+        h = _lib.orc_checkpoint(self._h)
+        if not h:
+            raise OracleError(-1, _lib.orc_last_error().decode())
+        return OracleState(h)
+
+    def restore(self, state: "OracleState") -> None:
+        _check(_lib.orc_restore(self._h, state._h))
+
     def kv_row(self, layer: int, is_v: bool, pos: int) -> np.ndarray:
         out = np.empty(self.width, np.float32)
         _check(_lib.orc_kv_row(self._h, layer, int(is_v), pos, _fp(out)))
@@ -190,6 +215,14 @@ def sample(processed: np.ndarray, rng_state: int, draws: int = 1) -> Tuple[List[
 def splitmix_sequence(seed: int, n: int) -> List[int]:
     st = C.c_uint64(seed & (2**64 - 1))
     return [int(_lib.orc_splitmix_next(C.byref(st))) for _ in range(n)]
+
+
+def libm_eval(fn: int, first: int, stride: int, count: int) -> np.ndarray:
+    """glibc's expf (0), exp of the float widened (1) or logf (2) on the floats with bit patterns
+    first + i * stride."""
+    out = np.empty(count, np.float64 if fn == 1 else np.float32)
+    _lib.orc_libm_eval(fn, first, stride, count, out.ctypes.data)
+    return out
 
 
 def gelu(v: float) -> float:

@@ -84,6 +84,18 @@ def timed(fn, reps: int):
     return out, times
 
 
+def batch8_inputs(it, dec):
+    """8 independent sequences: 32 latents + U[24, 200] text ids (lengths from seed 7, inputs seed
+    100 + b), 300 sampled codes each with the default options and seed 1000 + b."""
+    rng = np.random.default_rng(7)
+    prefixes, opts = [], []
+    for b in range(8):
+        cond, text = it.synthetic_prefix_inputs(int(rng.integers(24, 201)), seed=100 + b)
+        prefixes.append(dec.prepare_cond(cond, text, 0))
+        opts.append(it.GenerationOptions(seed=1000 + b, suppress_stop=True))
+    return prefixes, opts
+
+
 def extras(it, dec, weights):
     """Beam-3, long-context, 8-segment request and batch-8 (FP32, BF16) workloads of the same model."""
     res = {}
@@ -116,13 +128,7 @@ def extras(it, dec, weights):
         "attention_at_2047_rows": {"avg_us": round(att["avg_ms"] * 1e3, 2),
                                    "GBps": round(att["bytes"] / (att["avg_ms"] * 1e-3) / 1e9, 1)},
     }
-    # 8 independent sequences: text lengths U[24, 200] (seed 7), 300 sampled codes each.
-    rng = np.random.default_rng(7)
-    prefixes, opts = [], []
-    for b in range(8):
-        cond, text = it.synthetic_prefix_inputs(int(rng.integers(24, 201)), seed=100 + b)
-        prefixes.append(dec.prepare_cond(cond, text, 0))
-        opts.append(it.GenerationOptions(seed=1000 + b, suppress_stop=True))
+    prefixes, opts = batch8_inputs(it, dec)
     # One request's text segments (NativeRuntime's loop, native_runtime.cpp:98-99): 8 segments
     # of U[24, 120] text ids (seed 11), speaker/emotion conditioning, 300 sampled codes each.
     # generate_segments decodes them together; the reference's loop runs them one at a time.
@@ -177,7 +183,8 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode; 'beam3': the beam-3 workload")
+    ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode; 'beam3': the beam-3 workload; "
+                         "'batch8' / 'batch8_bf16': the 8-sequence workload")
     ap.add_argument("--iters", type=int, default=240)
     ap.add_argument("--kernel-batch", type=int, default=1, help="sequences per launch for --kernel-only")
     args = ap.parse_args()
@@ -200,6 +207,18 @@ def main() -> int:
         print(json.dumps({"kernel": "beam3", "codes": len(r.codes), "beam_steps": tm["decode_steps"],
                           "beam_tokens_per_s": round(3 * tm["decode_steps"] / (tm["decode_ms"] * 1e-3), 2),
                           "ms_per_beam_step": round(tm["decode_ms"] / tm["decode_steps"], 4)}), flush=True)
+        return 0
+    if args.kernel_only in ("batch8", "batch8_bf16"):
+        # the extras' batch-8 workload alone (8 ragged sequences x 300 sampled codes), for profilers
+        d = dec if args.kernel_only == "batch8" else it.GptDecoder(weights, kv_capacity=4096, max_batch=8, weight_dtype="bf16")
+        prefixes, opts = batch8_inputs(it, d)
+        d.generate_batch(prefixes, opts, 16)
+        r = d.generate_batch(prefixes, opts, 300)
+        tm = d.last_timing()
+        print(json.dumps({"kernel": args.kernel_only, "codes": sum(len(x.codes) for x in r), "decode_steps": tm["decode_steps"],
+                          "decode_tokens_per_s": round(8 * (tm["decode_steps"] - 1) / (tm["decode_ms"] * 1e-3), 2),
+                          "ms_per_step": round(tm["decode_ms"] / max(1, tm["decode_steps"] - 1), 4),
+                          "prefill_ms": round(tm["prefill_ms"], 3)}), flush=True)
         return 0
     if args.kernel_only == "codec":
         codec = it.EnhancedCodec(it.make_synthetic_codec_weights(seed=0))

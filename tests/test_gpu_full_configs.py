@@ -1,0 +1,214 @@
+"""Full-size parity of the HIP path on the 24-layer d=1280 FP32 GPT (MI355X).
+
+The workloads bench.py times, against the CPU oracle:
+  * 155-row prefix, 600 sampled codes (KV to 754): codes exact; teacher-forced logits at every
+    step against the oracle run live on the host; at every step the device sampler, given the
+    device's own logits and the oracle's SplitMix64 state, picks the oracle's code;
+  * 235-row prefix, greedy to 1813 codes (KV to 2047, attention beyond 16 splits): codes exact on
+    the persistent step and on the multi-kernel path, whose logits agree bit for bit at every
+    step; teacher-forced logits against the oracle's fixture at the stored steps;
+  * 8 ragged sequences x 300 sampled codes: codes exact with FP32 weights; BF16-stored weights
+    held to a stated logit tolerance against the FP32 oracle.
+Expected codes and fixture logits: tests/golden/full_configs.npz, written by
+tests/golden/make_full_config_golden.py.
+
+Logit bars: the path's bar (max-abs 1e-3, L2-relative 1e-4, argmax equal) at every compared
+step, and the reference's own gpt_test bar (max-abs < 1e-4, RMSE < 2e-5, src/main.cpp:47-48)
+asserted at every compared step as well; the achieved worst case is printed.
+"""
+import os
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "full_configs.npz"
+LOGIT_ABS, LOGIT_REL = 1e-3, 1e-4
+REF_ABS, REF_RMSE = 1e-4, 2e-5   # src/main.cpp:47 (compare(name, logits, ref, 1e-4f, 2e-5))
+BF16_ABS = 5e-2                  # BF16-stored weights, FP32 accumulate, against the FP32 oracle
+
+
+class Errors:
+    """Worst logit errors over the compared steps; check() asserts both bars on them."""
+
+    def __init__(self, what):
+        self.what, self.n = what, 0
+        self.worst = {"abs": (0.0, None), "rel": (0.0, None), "rmse": (0.0, None)}
+        self.argmax_bad = []
+
+    def add(self, got, ref, step):
+        d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+        for k, v in (("abs", float(d.max())), ("rel", rel_err(got, ref)), ("rmse", float(np.sqrt(np.mean(d * d))))):
+            if v > self.worst[k][0]:
+                self.worst[k] = (v, step)
+        if int(np.argmax(got)) != int(np.argmax(ref)):
+            self.argmax_bad.append(step)
+        self.n += 1
+
+    def check(self):
+        (a, sa), (r, sr), (rm, srm) = self.worst["abs"], self.worst["rel"], self.worst["rmse"]
+        print(f"{self.what}: {self.n} steps, worst max-abs {a:.3e} (step {sa}), rel {r:.3e} (step {sr}), "
+              f"rmse {rm:.3e} (step {srm})", flush=True)
+        assert not self.argmax_bad, f"{self.what}: argmax differs at steps {self.argmax_bad[:10]}"
+        assert a <= LOGIT_ABS and r <= LOGIT_REL, f"{self.what}: max-abs {a:.3e} rel {r:.3e}"
+        assert a < REF_ABS and rm < REF_RMSE, f"{self.what}: reference bar, max-abs {a:.3e} rmse {rm:.3e}"
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def _suppressed(lg):
+    out = lg.copy()
+    out[8192] = out[8193] = -np.inf  # suppress_stop: raw logits 8192, 8193 -> -inf before the processors
+    return out
+
+
+def test_config2_sampled_600(itts, oracle, full_weights, golden):
+    codes = [int(c) for c in golden["c2.codes"]]
+    dec = itts.GptDecoder(full_weights, kv_capacity=4096)
+    orc = oracle.OracleGpt(full_weights, kv_capacity=4096)
+    cond, text = itts.synthetic_prefix_inputs(120, seed=42)
+    prefix = dec.prepare_cond(cond, text, 0)
+    assert prefix.size // 1280 == 155
+    opts = dict(do_sample=True, seed=42, temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=10.0)
+    o = itts.GenerationOptions(suppress_stop=True, **opts)
+    print("config 2: generate 600", flush=True)
+    r = dec.generate(prefix, o, 600)
+    assert dec.last_timing()["decode_path"] == "step"
+    assert len(r.codes) == 600 and not r.stopped
+    assert r.codes == codes, f"first divergence at {next(i for i, (a, b) in enumerate(zip(r.codes, codes)) if a != b)}"
+
+    print("config 2: teacher-forced replay, device vs live oracle", flush=True)
+    err = Errors("config 2 logits")
+    proc_opts = itts.GenerationOptions(**opts)
+    history, rng = [1, 8192], 42
+    fixture = dict(zip([int(s) for s in golden["c2.steps"]], golden["c2.logits"]))
+    for t in range(600):
+        got = dec.prefill(prefix) if t == 0 else dec.step(codes[t - 1], t + 1)
+        ref = orc.prefill(prefix) if t == 0 else orc.step(codes[t - 1], t + 1)
+        if t in fixture:
+            assert np.array_equal(ref, fixture[t]), f"live oracle != fixture at step {t}"
+        err.add(got, ref, t)
+        # the device sampler on the device's logits, with the oracle's RNG state at this step
+        toks, rng = itts.sample_gpt_token(itts.apply_gpt_sampling_processors(_suppressed(got), history, proc_opts), rng, 1)
+        assert toks[0] == codes[t], f"step {t}: device sampler picked {toks[0]}, oracle {codes[t]}"
+        history.append(codes[t])
+    err.check()
+    assert dec.cached_tokens() == 155 + 599
+    dec.close()
+
+
+def _greedy_divergence(what, got_codes, exp_codes):
+    i = next((i for i, (a, b) in enumerate(zip(got_codes, exp_codes)) if a != b), None)
+    assert i is None and len(got_codes) == len(exp_codes), f"{what}: codes differ first at {i}"
+
+
+def test_config4_long_context_greedy(itts, full_weights, golden):
+    codes = [int(c) for c in golden["c4.codes"]]
+    old = os.environ.get("ITTS_GPT_PERSISTENT")
+    try:
+        os.environ["ITTS_GPT_PERSISTENT"] = "0"
+        multi = itts.GptDecoder(full_weights, kv_capacity=4096)
+        os.environ["ITTS_GPT_PERSISTENT"] = "1"
+        step = itts.GptDecoder(full_weights, kv_capacity=4096)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT"] = old
+    cond, text = itts.synthetic_prefix_inputs(200, seed=4)
+    prefix = step.prepare_cond(cond, text, 0)
+    assert prefix.size // 1280 == 235
+    o = itts.GenerationOptions(do_sample=False, repetition_penalty=1.0, suppress_stop=True)
+    for dec, path in ((step, "step"), (multi, "multi")):
+        print(f"config 4: generate 1813 on the {path} path", flush=True)
+        r = dec.generate(prefix, o, 1813)
+        assert dec.last_timing()["decode_path"] == path
+        _greedy_divergence(f"config 4 ({path})", r.codes, codes)
+        assert dec.cached_tokens() == 235 + 1812
+
+    print("config 4: teacher-forced replay on both paths", flush=True)
+    err = Errors("config 4 logits")
+    fixture = dict(zip([int(s) for s in golden["c4.steps"]], golden["c4.logits"]))
+    for t in range(1813):
+        a = step.prefill(prefix) if t == 0 else step.step(codes[t - 1], t + 1)
+        b = multi.prefill(prefix) if t == 0 else multi.step(codes[t - 1], t + 1)
+        assert np.array_equal(a, b), f"step {t} ({235 + t} cached rows): persistent != multi-kernel, max diff {np.max(np.abs(a - b))}"
+        if t < 1812:
+            assert int(np.argmax(a[:8192])) == codes[t]
+        if t in fixture:
+            err.add(a, fixture[t], t)
+    err.check()
+    assert step.cached_tokens() == 2047
+    step.close()
+    multi.close()
+
+
+def _c5_prefixes(itts, dec):
+    rng = np.random.default_rng(7)
+    out = []
+    for b in range(8):
+        cond, text = itts.synthetic_prefix_inputs(int(rng.integers(24, 201)), seed=100 + b)
+        out.append(dec.prepare_cond(cond, text, 0))
+    return out
+
+
+def test_config5_batch8_fp32(itts, full_weights, golden):
+    dec = itts.GptDecoder(full_weights, kv_capacity=4096, max_batch=8)
+    prefixes = _c5_prefixes(itts, dec)
+    assert [p.size // 1280 for p in prefixes] == [int(x) for x in golden["c5.rows"]]
+    opts = [itts.GenerationOptions(seed=1000 + b, suppress_stop=True) for b in range(8)]
+    print("config 5: generate_batch 8 x 300 (FP32)", flush=True)
+    res = dec.generate_batch(prefixes, opts, 300)
+    for b in range(8):
+        assert res[b].codes == [int(c) for c in golden["c5.codes"][b]], f"sequence {b}"
+    err = Errors("config 5 logits")
+    steps = [int(s) for s in golden["c5.steps"]]
+    for b in range(8):
+        codes = [int(c) for c in golden["c5.codes"][b]]
+        for k, t in enumerate(steps):
+            if t == 0:
+                got = dec.prefill(prefixes[b])
+            else:
+                if k == 0 or steps[k - 1] != t - 1:  # replay from the prefill up to step t
+                    dec.prefill(prefixes[b])
+                    for u in range(1, t):
+                        dec.step(codes[u - 1], u + 1)
+                got = dec.step(codes[t - 1], t + 1)
+            err.add(got, golden["c5.logits"][b][k], (b, t))
+    err.check()
+    dec.close()
+
+
+def test_config5_batch8_bf16_tolerance(itts, full_weights, golden):
+    """BF16-stored weights (round to nearest even at load, FP32 accumulate): logits along the FP32
+    oracle's codes within BF16_ABS max-abs of the FP32 oracle at the stored steps of all 8
+    sequences; the 8 x 300 batch runs to length (its codes differ from FP32's, as the sampler
+    sees different logits)."""
+    dec = itts.GptDecoder(full_weights, kv_capacity=4096, max_batch=8, weight_dtype="bf16")
+    prefixes = _c5_prefixes(itts, dec)
+    opts = [itts.GenerationOptions(seed=1000 + b, suppress_stop=True) for b in range(8)]
+    print("config 5: generate_batch 8 x 300 (BF16)", flush=True)
+    res = dec.generate_batch(prefixes, opts, 300)
+    assert all(len(r.codes) == 300 for r in res)
+    steps = [int(s) for s in golden["c5.steps"]]
+    worst, worst_rmse = 0.0, 0.0
+    for b in range(8):
+        codes = [int(c) for c in golden["c5.codes"][b]]
+        got = {0: dec.prefill(prefixes[b])}
+        for t in range(1, max(steps) + 1):
+            lg = dec.step(codes[t - 1], t + 1)
+            if t in steps:
+                got[t] = lg
+        for k, t in enumerate(steps):
+            d = np.abs(got[t].astype(np.float64) - golden["c5.logits"][b][k])
+            worst, worst_rmse = max(worst, float(d.max())), max(worst_rmse, float(np.sqrt(np.mean(d * d))))
+    print(f"config 5 BF16 vs FP32 oracle: worst max-abs {worst:.3e}, rmse {worst_rmse:.3e} (bar {BF16_ABS})", flush=True)
+    assert worst < BF16_ABS
+    dec.close()

@@ -148,6 +148,17 @@ void itts_gpt_state_release(itts_gpt_state* state);
 int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options,
                       uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped);
 
+/* No counterpart in the reference: itts_gpt_generate (one sequence, num_beams 1) for callers
+ * that cannot allocate device memory (tight serving loops, harnesses that forbid hipMalloc).
+ * It calls no hipMalloc/hipFree: the prefill activations live in a 20 MiB device array of
+ * the library (one per GPU, held until the process ends) instead of buffers grown per call,
+ * and a decode graph not captured yet is replaced by eager launches of the same kernels.
+ * Same kernels, same codes as itts_gpt_generate.  Limits (ITTS_EINVAL): prefix rows <= 512,
+ * num_beams == 1.  Calls on one GPU share that array: within a process they are serialised
+ * by a lock; the array keeps the last call's contents. */
+int itts_gpt_generate_noalloc(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options,
+                              uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped);
+
 /* Independent requests decoded together (no reference counterpart: the reference
  * runs one request at a time, http.cpp:57).  Sequence b's prefix is prefixes[b]
  * (rows[b] x 1280); each follows generate()'s semantics with options[b].

@@ -236,6 +236,11 @@ hipError_t launch_text_rows(const float* text_emb, const float* text_pos, const 
 // Speaker conditioning row (gpt.cpp:53-54): out = (bias + W speaker) + emotion.
 hipError_t launch_speaker_row(const float* w, const float* b, const float* speaker, const float* emotion, float* out,
                               hipStream_t s);
+// seen[b][i] = (i == 1 || i == 8192) for sequences b < nseq: the history {1, 8192}.
+hipError_t launch_seen_reset(uint8_t* seen, int nseq, hipStream_t s);
+// Prefill rows of one sequence in slot 0: row_slot[r] = 0, row_pos[r] = r (r < rows),
+// last_rows[0] = rows - 1, last_rows[1..kMaxBatch) = 0.
+hipError_t launch_prefill_rows_one(uint32_t* row_slot, uint32_t* row_pos, uint32_t* last_rows, uint32_t rows, hipStream_t s);
 // Copy row src_rows[b] of x into h[b] (last prefix row of each sequence).
 hipError_t launch_gather_rows(const float* x, const uint32_t* src_rows, float* h, int batch, hipStream_t s);
 // Beam reorder: child c (of `children`) takes parent[c]'s row owners for rows 0..n-1 and its

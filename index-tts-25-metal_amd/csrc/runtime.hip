@@ -129,7 +129,66 @@ hipError_t launch_step_serialized(const StepArgs& a, int nseq, int grid, bool bf
     return hipEventRecord(it->second, s);
 }
 
+// ---------------------------------------------------------------- scratch of generate_noalloc
+// itts_gpt_generate_noalloc takes the prefill's activations (which itts_gpt_generate grows
+// with hipMalloc as prefixes get longer) from this file-scope device array instead, so the
+// call allocates nothing.  Layout for M <= kNoAllocRows prefix rows, every part 256-B aligned:
+//   x, xn, q, att [kNoAllocRows][1280] f32; ff [kNoAllocRows][5120] f32;
+//   row_slot, row_pos [kNoAllocRows] u32; last_rows [64] u32.
+// Each GPU holds its own copy (20 MiB) until the process ends.  Host code never passes the
+// array's name to a kernel: it is a host-side stand-in there.  The device address, per
+// device, comes from hipGetSymbolAddress at decoder creation (scratch_address below).
+constexpr uint32_t kNoAllocRows = 512;
+constexpr size_t kScratchActBytes = size_t(kNoAllocRows) * kWidth * 4;
+constexpr size_t kScratchOffX = 0;
+constexpr size_t kScratchOffXn = kScratchOffX + kScratchActBytes;
+constexpr size_t kScratchOffQ = kScratchOffXn + kScratchActBytes;
+constexpr size_t kScratchOffAtt = kScratchOffQ + kScratchActBytes;
+constexpr size_t kScratchOffFf = kScratchOffAtt + kScratchActBytes;
+constexpr size_t kScratchOffSlot = kScratchOffFf + size_t(kNoAllocRows) * kFfn * 4;
+constexpr size_t kScratchOffPos = kScratchOffSlot + size_t(kNoAllocRows) * 4;
+constexpr size_t kScratchOffLast = kScratchOffPos + size_t(kNoAllocRows) * 4;
+constexpr size_t kScratchBytes = kScratchOffLast + 64 * 4;
+static_assert(kScratchOffXn % 256 == 0 && kScratchOffFf % 256 == 0 && kScratchOffSlot % 256 == 0 &&
+                  kScratchOffPos % 256 == 0 && kScratchOffLast % 256 == 0 && kMaxBatch <= 64,
+              "scratch parts must stay 256-B aligned");
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Per device: the address of `scratch` there, and a lock that serialises the no-alloc calls
+// of this process on that device (they share the one array).  Filled once per device.
+struct ScratchEntry {
+    uint8_t* ptr = nullptr;
+    std::string error;
+    std::unique_ptr<std::mutex> lock;
+};
+std::mutex g_scratch_mu;
+std::unordered_map<int, ScratchEntry> g_scratch;
+
+// Looks `scratch` up on device `dev`, which must be current.  A failure is recorded, not
+// thrown: only itts_gpt_generate_noalloc needs the address, and it reports the error.
+ScratchEntry* scratch_entry(int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch.find(dev);
+    if (it != g_scratch.end()) return &it->second;
+    ScratchEntry e;
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+        e.error = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(err);
+    else
+        e.ptr = static_cast<uint8_t*>(p);
+    e.lock = std::make_unique<std::mutex>();
+    return &g_scratch.emplace(dev, std::move(e)).first->second;
+}
+
 }  // namespace
+
+// Device buffers of one prefill (enqueue_prefill_layers).
+struct PrefillBufs {
+    float *x, *xn, *q, *att, *ff;
+    uint32_t *row_slot, *row_pos, *last_rows;
+};
 
 struct Engine {
     // ---------------------------------------------------------------- model
@@ -198,6 +257,10 @@ struct Engine {
     uint32_t cached = 0;
     itts_gpt_timing timing{};
     std::string last_error;
+    // itts_gpt_generate_noalloc: this device's `scratch` entry (address or lookup error), and
+    // whether the call in progress must not allocate (no graph capture, no buffer growth).
+    ScratchEntry* scratch_dev = nullptr;
+    bool no_alloc_call = false;
 
     ~Engine() {
         // Queued work may still write this handle's buffers (a beam search that raised with
@@ -374,6 +437,9 @@ struct Engine {
         table.alloc(B * cap);
         table_tmp.alloc(B * cap);
         init_step();
+        int dev = 0;
+        HIP_CHECK(hipGetDevice(&dev));
+        scratch_dev = scratch_entry(dev);
         HIP_CHECK(hipStreamSynchronize(stream));
     }
 
@@ -592,7 +658,9 @@ struct Engine {
             return;
         }
         timing.decode_path = ITTS_PATH_MULTI;
-        if (use_graphs) {
+        // A call that must not allocate replays a graph only if it was captured earlier
+        // (capture and instantiation allocate); otherwise it launches the same kernels eagerly.
+        if (use_graphs && (!no_alloc_call || graphs.count(std::make_tuple(nseq, nb, sampler, use_table)))) {
             HIP_CHECK(hipGraphLaunch(graph(nseq, nb, sampler, use_table), stream));
             return;
         }
@@ -656,67 +724,75 @@ struct Engine {
         HIP_CHECK(hipMemcpyAsync(last_rows.p, last.data(), kMaxBatch * 4, hipMemcpyHostToDevice, stream));
         // Host vectors above must outlive the async copies.
         HIP_CHECK(hipStreamSynchronize(stream));
+        enqueue_prefill_layers(PrefillBufs{px.p, pxn.p, pq.p, patt.p, pff.p, row_slot.p, row_pos.p, last_rows.p}, nseq, M);
+    }
+
+    // The prefill forward over M stacked rows whose inputs are in b.x, with each row's
+    // sequence slot and position in b.row_slot / b.row_pos and each sequence's last row in
+    // b.last_rows; leaves the last rows' logits in logits[0..nseq).
+    void enqueue_prefill_layers(const PrefillBufs& b, int nseq, uint32_t M) {
+        float *px_ = b.x, *pxn_ = b.xn, *pq_ = b.q, *patt_ = b.att, *pff_ = b.ff;
         for (int l = 0; l < layers; ++l) {
             const float* par = params.p + static_cast<size_t>(l) * kParLayer;
-            HIP_CHECK(launch_ln_rows(LnRowsArgs{px.p, pxn.p, par + kParLn1W, par + kParLn1B, static_cast<int>(M)}, stream));
+            HIP_CHECK(launch_ln_rows(LnRowsArgs{px_, pxn_, par + kParLn1W, par + kParLn1B, static_cast<int>(M)}, stream));
             GemmArgs g{};
-            g.a = pxn.p;
+            g.a = pxn_;
             g.w = w_ptr(off_qkv[l]);
             g.bias = par + kParQkvB;
             g.M = static_cast<int>(M);
             g.N = kQkv;
             g.K = kWidth;
-            g.c = pq.p;
+            g.c = pq_;
             g.kv = kv.p;
             g.kv_slot_stride = kv_slot_stride;
             g.kv_layer_off = kv_layer_off(l);
             g.kv_v_off = kv_v_off;
             g.kv_cap = cap;
-            g.row_slot = row_slot.p;
-            g.row_pos = row_pos.p;
+            g.row_slot = b.row_slot;
+            g.row_pos = b.row_pos;
             HIP_CHECK(launch_gemm(g, kGemmQkv, bf16, stream));
             CausalArgs c{};
-            c.q = pq.p;
+            c.q = pq_;
             c.kv = kv.p;
             c.kv_slot_stride = kv_slot_stride;
             c.kv_layer_off = kv_layer_off(l);
             c.kv_v_off = kv_v_off;
             c.kv_cap = cap;
-            c.row_slot = row_slot.p;
-            c.row_pos = row_pos.p;
-            c.out = patt.p;
+            c.row_slot = b.row_slot;
+            c.row_pos = b.row_pos;
+            c.out = patt_;
             c.M = static_cast<int>(M);
             HIP_CHECK(launch_causal_attention(c, stream));
             GemmArgs p{};
-            p.a = patt.p;
+            p.a = patt_;
             p.w = w_ptr(off_proj[l]);
             p.bias = par + kParProjB;
             p.M = static_cast<int>(M);
             p.N = kWidth;
             p.K = kWidth;
-            p.c = px.p;
+            p.c = px_;
             HIP_CHECK(launch_gemm(p, kGemmResid, bf16, stream));
-            HIP_CHECK(launch_ln_rows(LnRowsArgs{px.p, pxn.p, par + kParLn2W, par + kParLn2B, static_cast<int>(M)}, stream));
+            HIP_CHECK(launch_ln_rows(LnRowsArgs{px_, pxn_, par + kParLn2W, par + kParLn2B, static_cast<int>(M)}, stream));
             GemmArgs f{};
-            f.a = pxn.p;
+            f.a = pxn_;
             f.w = w_ptr(off_fc[l]);
             f.bias = par + kParFcB;
             f.M = static_cast<int>(M);
             f.N = kFfn;
             f.K = kWidth;
-            f.c = pff.p;
+            f.c = pff_;
             HIP_CHECK(launch_gemm(f, kGemmGelu, bf16, stream));
             GemmArgs f2{};
-            f2.a = pff.p;
+            f2.a = pff_;
             f2.w = w_ptr(off_fc2[l]);
             f2.bias = par + kParFc2B;
             f2.M = static_cast<int>(M);
             f2.N = kWidth;
             f2.K = kFfn;
-            f2.c = px.p;
+            f2.c = px_;
             HIP_CHECK(launch_gemm(f2, kGemmResid, bf16, stream));
         }
-        HIP_CHECK(launch_gather_rows(px.p, last_rows.p, h.p, nseq, stream));
+        HIP_CHECK(launch_gather_rows(px_, b.last_rows, h.p, nseq, stream));
         enqueue_head(nseq, gemv_batch_bucket(nseq));
     }
 
@@ -795,21 +871,14 @@ struct Engine {
             throw std::invalid_argument("Invalid beam search configuration");
     }
 
-    void reset_seen(int nseq) {
-        std::vector<uint8_t> s(static_cast<size_t>(nseq) * kMelVocab, 0);
-        for (int b = 0; b < nseq; ++b) {
-            s[static_cast<size_t>(b) * kMelVocab + 1] = 1;  // history {1, 8192} (gpt_sampling.cpp:176)
-            s[static_cast<size_t>(b) * kMelVocab + kMelStart] = 1;
-        }
-        HIP_CHECK(hipMemcpyAsync(seen.p, s.data(), s.size(), hipMemcpyHostToDevice, stream));
-        HIP_CHECK(hipStreamSynchronize(stream));
-    }
+    // Repetition sets of sequences 0..nseq-1 = the history {1, 8192} (gpt_sampling.cpp:176).
+    void reset_seen(int nseq) { HIP_CHECK(launch_seen_reset(seen.p, nseq, stream)); }
 
     // Device-driven decode loop for nseq independent sequences whose prefill logits
     // are in logits[0..nseq): sampler, then (forward + sampler) graph replays.
     void decode_loop(int nseq, uint32_t max_tokens) {
         const int nb = gemv_batch_bucket(nseq);
-        if (use_graphs && !persistent(nseq, false)) (void)graph(nseq, nb, true, false);  // captured before any work is queued
+        if (use_graphs && !no_alloc_call && !persistent(nseq, false)) (void)graph(nseq, nb, true, false);  // captured before any work is queued
         HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
         constexpr uint32_t kChunk = 16;
         uint32_t launched = 0;
@@ -850,10 +919,16 @@ struct Engine {
         enqueue_prefill(prefixes, rows);
         HIP_CHECK(hipEventRecord(ev[1], stream));
         decode_loop(nseq, max_tokens);
+        finish_generation(nseq, max_tokens, codes_out, n_codes, stopped);
+    }
+
+    // After decode_loop: timings, errors and the codes of sequences 0..nseq-1 (statuses are
+    // staged in pinned[32..32+nseq); decode_loop uses pinned[0..32)).
+    void finish_generation(int nseq, uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
         HIP_CHECK(hipEventRecord(ev[2], stream));
         HIP_CHECK(hipMemcpyAsync(pinned_state, state.p, nseq * sizeof(SeqState), hipMemcpyDeviceToHost, stream));
-        std::vector<uint32_t> st(nseq);
-        HIP_CHECK(hipMemcpyAsync(st.data(), status.p, nseq * 4, hipMemcpyDeviceToHost, stream));
+        uint32_t* st = pinned + 32;
+        HIP_CHECK(hipMemcpyAsync(st, status.p, nseq * 4, hipMemcpyDeviceToHost, stream));
         HIP_CHECK(hipStreamSynchronize(stream));
         HIP_CHECK(hipEventElapsedTime(&timing.prefill_ms, ev[0], ev[1]));
         HIP_CHECK(hipEventElapsedTime(&timing.decode_ms, ev[1], ev[2]));
@@ -871,6 +946,45 @@ struct Engine {
         timing.decode_steps = steps;
         const SeqState& s0 = pinned_state[0];
         cached = s0.prefix_rows + (s0.stopped ? s0.count : (s0.count ? s0.count - 1 : 0));
+    }
+
+    // generate() for one sequence (num_beams 1) without allocating: the prefill activations
+    // live in this device's `scratch` array (prefixes up to kNoAllocRows rows), the decode
+    // loop uses the buffers allocated at creation, and a decode graph not captured yet is
+    // replaced by eager launches of the same kernels.  Same kernels, same codes as generate().
+    void generate_noalloc(const float* prefix, uint32_t rows, const itts_gen_options& opt, uint32_t max_tokens,
+                          uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
+        itts_gen_options c = opt;
+        check_prefix(rows);
+        validate_generation(c, max_tokens, rows, mel_pos_rows, cap);
+        if (c.num_beams != 1)
+            throw std::invalid_argument("itts_gpt_generate_noalloc decodes one sequence without beams (num_beams 1)");
+        if (rows > kNoAllocRows)
+            throw std::invalid_argument("itts_gpt_generate_noalloc: the prefix exceeds the 512-row scratch");
+        if (!scratch_dev || !scratch_dev->ptr)
+            throw std::runtime_error("itts_gpt_generate_noalloc: no scratch on this device" +
+                                     (scratch_dev ? ": " + scratch_dev->error : std::string()));
+        std::lock_guard<std::mutex> lock(*scratch_dev->lock);
+        uint8_t* base = scratch_dev->ptr;
+        const PrefillBufs b{reinterpret_cast<float*>(base + kScratchOffX),      reinterpret_cast<float*>(base + kScratchOffXn),
+                            reinterpret_cast<float*>(base + kScratchOffQ),      reinterpret_cast<float*>(base + kScratchOffAtt),
+                            reinterpret_cast<float*>(base + kScratchOffFf),     reinterpret_cast<uint32_t*>(base + kScratchOffSlot),
+                            reinterpret_cast<uint32_t*>(base + kScratchOffPos), reinterpret_cast<uint32_t*>(base + kScratchOffLast)};
+        struct Flag {  // cleared on every exit, errors included
+            bool& f;
+            explicit Flag(bool& x) : f(x) { f = true; }
+            ~Flag() { f = false; }
+        } flag(no_alloc_call);
+        pinned_state[0] = make_state(c, rows, max_tokens);
+        upload_states(1);
+        reset_seen(1);
+        HIP_CHECK(hipEventRecord(ev[0], stream));
+        HIP_CHECK(hipMemcpyAsync(b.x, prefix, static_cast<size_t>(rows) * kWidth * 4, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(launch_prefill_rows_one(b.row_slot, b.row_pos, b.last_rows, rows, stream));
+        enqueue_prefill_layers(b, 1, rows);
+        HIP_CHECK(hipEventRecord(ev[1], stream));
+        decode_loop(1, max_tokens);
+        finish_generation(1, max_tokens, codes_out, n_codes, stopped);
     }
 
     void generate(const float* prefix, uint32_t rows, const itts_gen_options& opt, uint32_t max_tokens, uint32_t* codes_out,
@@ -1541,6 +1655,14 @@ int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itt
     return guarded(h, [&] {
         if (!prefix) throw std::invalid_argument("Invalid GPT prefill dimensions");
         h->e.generate(prefix, rows, *options, max_tokens, codes_out, n_codes, stopped);
+    });
+}
+
+int itts_gpt_generate_noalloc(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options,
+                              uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped) {
+    return guarded(h, [&] {
+        if (!prefix || !options || !codes_out || !n_codes || !stopped) throw std::invalid_argument("Invalid GPT prefill dimensions");
+        h->e.generate_noalloc(prefix, rows, *options, max_tokens, codes_out, n_codes, stopped);
     });
 }
 

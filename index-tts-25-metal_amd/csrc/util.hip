@@ -94,7 +94,35 @@ __global__ void beam_apply_kernel(uint8_t* table, const uint8_t* table_tmp, uint
         seen[static_cast<size_t>(c) * kMelVocab + i] = i == tok ? 1 : seen_tmp[static_cast<size_t>(p) * kMelVocab + i];
 }
 
+// Repetition sets of sequences 0..grid.y-1: exactly {1, 8192} (gpt_sampling.cpp:176).
+__global__ void seen_reset_kernel(uint8_t* seen) {
+    uint8_t* row = seen + static_cast<size_t>(blockIdx.y) * kMelVocab;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kMelVocab; i += gridDim.x * blockDim.x)
+        row[i] = (i == 1 || i == kMelStart) ? 1 : 0;
+}
+
+// One sequence's prefill rows: slot 0, positions 0..rows-1, last row rows-1 (other
+// sequences' last-row entries 0).
+__global__ void prefill_rows_one_kernel(uint32_t* row_slot, uint32_t* row_pos, uint32_t* last_rows, uint32_t rows) {
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+        row_slot[r] = 0;
+        row_pos[r] = r;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < static_cast<unsigned>(kMaxBatch)) last_rows[threadIdx.x] = threadIdx.x == 0 ? rows - 1 : 0;
+}
+
 }  // namespace
+
+hipError_t launch_seen_reset(uint8_t* seen, int nseq, hipStream_t s) {
+    hipLaunchKernelGGL(seen_reset_kernel, dim3(8, nseq), dim3(256), 0, s, seen);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_rows_one(uint32_t* row_slot, uint32_t* row_pos, uint32_t* last_rows, uint32_t rows, hipStream_t s) {
+    hipLaunchKernelGGL(prefill_rows_one_kernel, dim3(std::max(1u, std::min(4u, (rows + 255) / 256))), dim3(256), 0, s, row_slot,
+                       row_pos, last_rows, rows);
+    return hipGetLastError();
+}
 
 hipError_t launch_transpose(const float* src, void* dst, int in, int out, bool bf16, hipStream_t s) {
     const dim3 grid((out + 31) / 32, (in + 31) / 32);

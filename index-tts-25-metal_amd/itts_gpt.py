@@ -96,6 +96,7 @@ def _load() -> C.CDLL:
         "itts_gpt_state_tokens": (u32, [P]),
         "itts_gpt_state_release": (None, [P]),
         "itts_gpt_generate": (C.c_int, [P, f32p, u32, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
+        "itts_gpt_generate_noalloc": (C.c_int, [P, f32p, u32, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
         "itts_gpt_generate_batch": (C.c_int, [P, u32, C.POINTER(f32p), u32p, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
         "itts_gpt_generate_segments": (C.c_int, [P, f32p, f32p, u32p, u32p, u32, u32, C.POINTER(_Options), u32, u32p, u32p,
                                                  C.POINTER(i32)]),
@@ -410,6 +411,17 @@ class GptDecoder:
         o = options._c()
         self._check(_lib.itts_gpt_generate(self._h, _fp(p), p.size // WIDTH, C.byref(o), int(max_tokens), _up(codes), C.byref(n),
                                            C.byref(stopped)))
+        return GenerationResult([int(c) for c in codes[: n.value]], bool(stopped.value))
+
+    def generate_noalloc(self, prefix: np.ndarray, options: GenerationOptions, max_tokens: int = 1500) -> GenerationResult:
+        """generate() through itts_gpt_generate_noalloc: no device allocation (prefix <= 512 rows, num_beams 1)."""
+        p = self._prefix(prefix)
+        codes = np.zeros(max(1, int(max_tokens)), np.uint32)
+        n = C.c_uint32()
+        stopped = C.c_int32()
+        o = options._c()
+        self._check(_lib.itts_gpt_generate_noalloc(self._h, _fp(p), p.size // WIDTH, C.byref(o), int(max_tokens), _up(codes),
+                                                   C.byref(n), C.byref(stopped)))
         return GenerationResult([int(c) for c in codes[: n.value]], bool(stopped.value))
 
     def generate_batch(self, prefixes: Sequence[np.ndarray], options, max_tokens: int) -> List[GenerationResult]:

@@ -49,12 +49,30 @@ def decode_bytes(prefix_rows: int, tokens: int) -> float:
     return total
 
 
+def prefill_flops(rows: int, layers: int = 24) -> float:
+    """FLOPs of a P-row prefill: the four GEMMs per layer (2 P N K), causal attention
+    (QK^T and PV over the lower triangle: 2 * 2 * 64 * P (P + 1) / 2 per head) and the head
+    GEMV of the last row."""
+    gemm = 2.0 * rows * (1280 * 3840 + 1280 * 1280 + 2 * 1280 * 5120)
+    attn = 20 * 2.0 * 64 * rows * (rows + 1)
+    return layers * (gemm + attn) + 2.0 * 8194 * 1280
+
+
 def cpu_baseline(weights, prefix, sample_steps: int):
     """The FP32 CPU oracle (OpenMP over output rows) on a bounded sample of the same decode."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    cpu_model = "unknown"
+    try:
+        import subprocess
+
+        for ln in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if ln.startswith("Model name:"):
+                cpu_model = ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     orc = oracle.OracleGpt(weights, kv_capacity=4096)
     t0 = time.perf_counter()
     orc.prefill(prefix)
@@ -70,6 +88,8 @@ def cpu_baseline(weights, prefix, sample_steps: int):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model,
+        "host_cpus": os.cpu_count(),
         "sample": f"oracle prefill of the 155-row prefix ({t1 - t0:.2f} s) then {sample_steps} decode steps "
                   f"(KV 155..{155 + sample_steps}) of the same 24-layer FP32 model, {t2 - t1:.1f} s",
     }
@@ -120,14 +140,28 @@ def extras(it, dec, weights):
     r, times = timed(lambda: dec.generate(prefix, o, 1813), 2)
     tm = dec.last_timing()
     rows = prefix.size // 1280
-    att = dec.bench_kernel("attention", iters=240, cached_rows=2046)
     res["long_context"] = {
         "codes": len(r.codes), "kv_rows": rows + len(r.codes) - 1,
         "decode_tokens_per_s": round((len(r.codes) - 1) / (tm["decode_ms"] * 1e-3), 2),
         "step_algorithmic_GBps": round(decode_bytes(rows, len(r.codes)) / (tm["decode_ms"] * 1e-3) / 1e9, 1),
-        "attention_at_2047_rows": {"avg_us": round(att["avg_ms"] * 1e3, 2),
-                                   "GBps": round(att["bytes"] / (att["avg_ms"] * 1e-3) / 1e9, 1)},
     }
+    if tm["decode_path"] == "step":
+        # the path that ran: the persistent step's attention phase (tiles + merge) at the last
+        # step (2046 cached rows + the new one), against its GEMV phases, from the kernel's stamps
+        ph = dec.step_phases(cached_rows=2046, iters=20)
+        att_us = ph["attention_tiles"] + ph["merge"]
+        gemv_us = ph["c_attn"] + ph["attn_proj"] + ph["mlp_fc"] + ph["mlp_proj"]
+        kv_layer = KV_BYTES_PER_ROW / 24 * 2047
+        w_layer = (WEIGHT_BYTES_PER_TOKEN - 41_953_280 - 32_776 - 20_480 - 10_240) / 24
+        res["long_context"]["persistent_step_at_2047_rows"] = {
+            "layer_us": round(ph["layer"], 2),
+            "attention_phase_us": round(att_us, 2), "attention_GBps": round(kv_layer / (att_us * 1e-6) / 1e9, 1),
+            "gemv_phases_us": round(gemv_us, 2), "gemv_GBps": round(w_layer / (gemv_us * 1e-6) / 1e9, 1),
+            "phases_us": {k: round(v, 2) for k, v in ph.items()},
+        }
+    att = dec.bench_kernel("attention", iters=240, cached_rows=2046)
+    res["long_context"]["multikernel_attention_kernel_at_2047_rows"] = {
+        "avg_us": round(att["avg_ms"] * 1e3, 2), "GBps": round(att["bytes"] / (att["avg_ms"] * 1e-3) / 1e9, 1)}
     prefixes, opts = batch8_inputs(it, dec)
     # One request's text segments (NativeRuntime's loop, native_runtime.cpp:98-99): 8 segments
     # of U[24, 120] text ids (seed 11), speaker/emotion conditioning, 300 sampled codes each.
@@ -180,11 +214,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=600)
-    ap.add_argument("--cpu-steps", type=int, default=256)
+    ap.add_argument("--cpu-steps", type=int, default=599, help="oracle decode steps (599: KV 155..754, the whole workload)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode; 'beam3': the beam-3 workload; "
-                         "'batch8' / 'batch8_bf16': the 8-sequence workload")
+                         "'batch8' / 'batch8_bf16': the 8-sequence workload; "
+                         "'prefill': the 155-row prefill")
     ap.add_argument("--iters", type=int, default=240)
     ap.add_argument("--kernel-batch", type=int, default=1, help="sequences per launch for --kernel-only")
     args = ap.parse_args()
@@ -207,6 +242,21 @@ def main() -> int:
         print(json.dumps({"kernel": "beam3", "codes": len(r.codes), "beam_steps": tm["decode_steps"],
                           "beam_tokens_per_s": round(3 * tm["decode_steps"] / (tm["decode_ms"] * 1e-3), 2),
                           "ms_per_beam_step": round(tm["decode_ms"] / tm["decode_steps"], 4)}), flush=True)
+        return 0
+    if args.kernel_only == "prefill":
+        # prefill of the headline's 155-row prefix, `iters` times (HIP-event time of each)
+        cond, text = it.synthetic_prefix_inputs(120, seed=42)
+        prefix = dec.prepare_cond(cond, text, 0)
+        dec.prefill(prefix)
+        ms = []
+        for _ in range(args.iters):
+            dec.prefill(prefix)
+            ms.append(dec.last_timing()["prefill_ms"])
+        rows = prefix.size // 1280
+        flops = prefill_flops(rows)
+        print(json.dumps({"kernel": "prefill", "rows": rows, "iters": args.iters, "avg_ms": round(float(np.mean(ms)), 4),
+                          "min_ms": round(float(np.min(ms)), 4), "GFLOP": round(flops / 1e9, 2),
+                          "TFLOPs": round(flops / (float(np.mean(ms)) * 1e-3) / 1e12, 2)}), flush=True)
         return 0
     if args.kernel_only in ("batch8", "batch8_bf16"):
         # the extras' batch-8 workload alone (8 ragged sequences x 300 sampled codes), for profilers
@@ -313,6 +363,8 @@ def main() -> int:
         },
         "kernels": per_kernel,
     }
+    if path == "step":
+        line["decode"]["step_phases_us_at_752_rows"] = {k: round(v, 2) for k, v in dec.step_phases(cached_rows=752, iters=20).items()}
     if not args.no_extras:
         line["extras"] = extras(it, dec, weights)
     del dec

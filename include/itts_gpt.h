@@ -150,7 +150,7 @@ int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itt
 
 /* No counterpart in the reference: itts_gpt_generate (one sequence, num_beams 1) for callers
  * that cannot allocate device memory (tight serving loops, harnesses that forbid hipMalloc).
- * It calls no hipMalloc/hipFree: the prefill activations live in a 20 MiB device array of
+ * It calls no hipMalloc/hipFree: the prefill activations live in a 28 MiB device array of
  * the library (one per GPU, held until the process ends) instead of buffers grown per call,
  * and a decode graph not captured yet is replaced by eager launches of the same kernels.
  * Same kernels, same codes as itts_gpt_generate.  Limits (ITTS_EINVAL): prefix rows <= 512,
@@ -220,6 +220,16 @@ int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
  * Attention and the step kernel run with `cached_rows` rows in the cache (0 -> 752). */
 int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t cached_rows, uint32_t iters, float* avg_ms,
                           double* bytes_per_launch);
+
+/* Measurement hook (no reference counterpart): where the persistent batch-1 step kernel's
+ * time goes at `cached_rows` cached rows (0 -> 752), from clock stamps the kernel writes at
+ * each phase end, averaged over `iters` launches.  phase_us[0] is the mean layer time;
+ * phase_us[1..6] the mean share of each phase of a layer on the critical path (c_attn +
+ * K/V append, attention tiles, split merge, attn.c_proj, mlp.c_fc, mlp.c_proj), measured
+ * from the last workgroup to finish the previous phase to the last to finish this one;
+ * phase_us[7] the head (ln_f, final_norm, mel_head).  FP32 decoders with the persistent
+ * path only. */
+int itts_gpt_step_phases(itts_gpt* h, uint32_t cached_rows, uint32_t iters, float* phase_us);
 
 /* ---- EnhancedCodec (src/codec.cpp), the consumer of the semantic codes ----------
  * The decode path of itts25::EnhancedCodec (include/itts25/codec.hpp:11-17) on the

@@ -120,7 +120,12 @@ struct StepArgs {
     size_t kv_slot_stride;
     int logit_stride;
     const uint8_t* table;     // beam row-owner table [nseq][kv_cap] (slot holding each row) or null
+    // measurement only (step.hip; null otherwise): workgroup b's clock at the phase ends of
+    // layer l, stamps[(b * (layers + 1) + l) * 8 + k], k = 0 layer start, 1 c_attn, 2 attention
+    // tiles, 3 merge, 4 attn.c_proj, 5 mlp.c_fc, 6 mlp.c_proj (l = layers: 0 head start, 6 head end)
+    uint64_t* stamps;
 };
+constexpr int kStepStampsPerLayer = 8;
 bool step_fits(int grid);
 hipError_t step_occupancy(bool bf16, int* blocks_per_cu);
 hipError_t launch_step(const StepArgs& a, int grid, bool bf16, hipStream_t s);
@@ -210,7 +215,18 @@ struct GemmArgs {
     uint32_t kv_cap;
     const uint32_t* row_slot;
     const uint32_t* row_pos;
+    // split-K: K is cut into `splits` equal ranges (a multiple of 16 each); the partial
+    // tiles go to ws[splits][M][N] and a second kernel adds them in split order
+    int splits;             // 1: no split
+    float* ws;
 };
+// Split-K is used while the output tiles number fewer than kGemmTargetTiles / 2: up to
+// kGemmMaxSplits splits, as many as keep tiles * splits <= kGemmTargetTiles.  The
+// workspace then holds splits * M * N <= kGemmTargetTiles * 64 * 64 floats.
+constexpr int kGemmTargetTiles = 512;
+constexpr int kGemmMaxSplits = 8;
+constexpr size_t kGemmWsFloats = size_t(kGemmTargetTiles) * 64 * 64;
+int gemm_splits(int M, int N, int K);
 hipError_t launch_gemm(const GemmArgs& a, int epi, bool bf16, hipStream_t s);
 
 struct CausalArgs {

@@ -6,7 +6,10 @@
 //   metal_context.mm:368-410.  64x64 tile per 256-thread workgroup, 2x2 waves of
 //   32x32, K staged through LDS 16 at a time with the next slab prefetched into
 //   registers.  Epilogues: q rows + K/V cache store (kernels.metal:1250-1266),
-//   residual add in place, GELU.
+//   residual add in place, GELU.  When the tiles alone would leave most CUs idle (a
+//   155-row prefix has 60 tiles of a 1280-wide output), K is split over gridDim.z:
+//   each split writes its partial tile to a workspace and gemm_reduce adds the splits
+//   in order, then the bias and the epilogue.
 // * causal_attention: one wave per (query row, head); 64 keys per pass, lane = key for
 //   the scores, lane = dimension for the weighted V sum, online max/sum rescaling
 //   (same recurrence as mit2_gpt_causal_attention_sgq_f32, kernels.metal:2249-2292).
@@ -33,7 +36,31 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(LnRowsArgs a) {
 
 constexpr int BM = 64, BN = 64, BK = 16, LDP = 4;
 
-template <typename WT, int EPI>
+// Output element (row, col) of the GEMM, v = dot + bias: the epilogue.
+template <int EPI>
+__device__ __forceinline__ void gemm_store(const GemmArgs& a, int row, int col, float v) {
+    if constexpr (EPI == kGemmQkv) {
+        if (col < kWidth) {
+            a.c[static_cast<size_t>(row) * kWidth + col] = v;
+        } else {
+            const int rr = col - kWidth;
+            const bool is_v = rr >= kWidth;
+            const int c = is_v ? rr - kWidth : rr;
+            const size_t off = static_cast<size_t>(a.row_slot[row]) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
+                               (static_cast<size_t>(c >> 6) * a.kv_cap + a.row_pos[row]) * kHeadDim + (c & 63);
+            a.kv[off] = v;
+        }
+    } else if constexpr (EPI == kGemmResid) {
+        float* p = a.c + static_cast<size_t>(row) * a.N + col;
+        *p = *p + v;
+    } else {
+        a.c[static_cast<size_t>(row) * a.N + col] = gelu_f(v);
+    }
+}
+
+// SPLIT: this workgroup covers K range [z Kz, (z + 1) Kz) of split z = blockIdx.z and
+// writes its raw partial tile to a.ws[z][M][N]; gemm_reduce_kernel finishes it.
+template <typename WT, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     __shared__ float As[BK][BM + LDP];
     __shared__ float Bs[BK][BN + LDP];
@@ -43,8 +70,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int lrow = tid >> 2, lk = (tid & 3) * 4;  // loader: one 4-wide K chunk of one row
     const int am = m0 + lrow;
     const bool arow_ok = am < a.M;
-    const float* arow = a.a + static_cast<size_t>(arow_ok ? am : 0) * a.K + lk;
-    const WT* wrow = static_cast<const WT*>(a.w) + static_cast<size_t>(n0 + lrow) * a.K + lk;
+    const int kz = SPLIT ? a.K / a.splits : a.K;  // this split's K extent, a multiple of BK
+    const int kbase = SPLIT ? static_cast<int>(blockIdx.z) * kz : 0;
+    const float* arow = a.a + static_cast<size_t>(arow_ok ? am : 0) * a.K + kbase + lk;
+    const WT* wrow = static_cast<const WT*>(a.w) + static_cast<size_t>(n0 + lrow) * a.K + kbase + lk;
 
     auto load_a = [&](int k0) -> float4 {
         return arow_ok ? *reinterpret_cast<const float4*>(arow + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -63,7 +92,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
     float4 ra = load_a(0), rb = load_b(0);
-    for (int k0 = 0; k0 < a.K; k0 += BK) {
+    for (int k0 = 0; k0 < kz; k0 += BK) {
         As[lk + 0][lrow] = ra.x;
         As[lk + 1][lrow] = ra.y;
         As[lk + 2][lrow] = ra.z;
@@ -73,7 +102,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         Bs[lk + 2][lrow] = rb.z;
         Bs[lk + 3][lrow] = rb.w;
         __syncthreads();
-        if (k0 + BK < a.K) {
+        if (k0 + BK < kz) {
             ra = load_a(k0 + BK);
             rb = load_b(k0 + BK);
         }
@@ -88,32 +117,37 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
     // D layout of v_mfma_f32_32x32x2f32: lane l, element i -> row 8(i/4) + 4(l/32) + i%4, col l%32.
     const int col = n0 + wn * 32 + (lane & 31);
-    const float bias = a.bias[col];
+    if constexpr (SPLIT) {
+        float* ws = a.ws + static_cast<size_t>(blockIdx.z) * a.M * a.N;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int row = m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row >= a.M) continue;
-        const float v = acc[i] + bias;
-        if constexpr (EPI == kGemmQkv) {
-            if (col < kWidth) {
-                a.c[static_cast<size_t>(row) * kWidth + col] = v;
-            } else {
-                const int rr = col - kWidth;
-                const bool is_v = rr >= kWidth;
-                const int c = is_v ? rr - kWidth : rr;
-                const size_t off = static_cast<size_t>(a.row_slot[row]) * a.kv_slot_stride + a.kv_layer_off +
-                                   (is_v ? a.kv_v_off : 0) + (static_cast<size_t>(c >> 6) * a.kv_cap + a.row_pos[row]) * kHeadDim +
-                                   (c & 63);
-                a.kv[off] = v;
-            }
-        } else if constexpr (EPI == kGemmResid) {
-            float* p = a.c + static_cast<size_t>(row) * a.N + col;
-            *p = *p + v;
-        } else {
-            a.c[static_cast<size_t>(row) * a.N + col] = gelu_f(v);
+        for (int i = 0; i < 16; ++i) {
+            const int row = m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            if (row < a.M) ws[static_cast<size_t>(row) * a.N + col] = acc[i];
+        }
+    } else {
+        const float bias = a.bias[col];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            if (row < a.M) gemm_store<EPI>(a, row, col, acc[i] + bias);
         }
     }
 }
+
+// Finishes a split-K GEMM: dot = partial 0 + partial 1 + ... in split order, then + bias and
+// the epilogue; one thread per output element.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a) {
+    const size_t total = static_cast<size_t>(a.M) * a.N, plane = total;
+    for (size_t e = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        float d = a.ws[e];
+        for (int z = 1; z < a.splits; ++z) d += a.ws[z * plane + e];
+        const int row = static_cast<int>(e / a.N), col = static_cast<int>(e % a.N);
+        gemm_store<EPI>(a, row, col, d + a.bias[col]);
+    }
+}
+
+__device__ __forceinline__ float lane_value_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 
 __global__ __launch_bounds__(64) void causal_attention_kernel(CausalArgs a) {
     const int m = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
@@ -148,10 +182,16 @@ __global__ __launch_bounds__(64) void causal_attention_kernel(CausalArgs a) {
         const float p = valid ? expf(s - mnew) : 0.0f;
         lrun = lrun * corr + wave_sum(p);
         acc *= corr;
+        // acc += p_k V[k] for the chunk's keys in order; 16 V rows in flight at a time, p_k read
+        // from lane k (a wave-uniform lane index)
         const int nk = min(64, pos + 1 - c0);
-        for (int k = 0; k < nk; ++k) {
-            const float pk = __shfl(p, k, 64);
-            acc = __builtin_fmaf(pk, vb[static_cast<size_t>(c0 + k) * kHeadDim + lane], acc);
+        for (int k0 = 0; k0 < nk; k0 += 16) {
+            float vv[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) vv[j] = k0 + j < nk ? vb[static_cast<size_t>(c0 + k0 + j) * kHeadDim + lane] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (k0 + j < nk) acc = __builtin_fmaf(lane_value_f(p, k0 + j), vv[j], acc);
         }
         mrun = mnew;
     }
@@ -165,10 +205,27 @@ hipError_t launch_ln_rows(const LnRowsArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+int gemm_splits(int M, int N, int K) {
+    const int tiles = (N / BN) * ((M + BM - 1) / BM);
+    int s = std::min(kGemmMaxSplits, std::max(1, kGemmTargetTiles / std::max(1, tiles)));
+    while (s > 1 && (K % (s * BK) != 0)) --s;
+    return s;
+}
+
 hipError_t launch_gemm(const GemmArgs& a, int epi, bool bf16, hipStream_t s) {
-    if (a.N % BN || a.K % BK) return hipErrorInvalidValue;
-    const dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
-#define ITTS_GEMM(WT, E) hipLaunchKernelGGL((gemm_kernel<WT, E>), grid, dim3(256), 0, s, a)
+    if (a.N % BN || a.K % BK || a.splits < 1 || a.K % (a.splits * BK) || (a.splits > 1 && !a.ws)) return hipErrorInvalidValue;
+    const bool split = a.splits > 1;
+    const dim3 grid(a.N / BN, (a.M + BM - 1) / BM, a.splits);
+    const int rblocks = static_cast<int>(std::min<size_t>((static_cast<size_t>(a.M) * a.N + 255) / 256, 2048));
+#define ITTS_GEMM(WT, E)                                                                       \
+    do {                                                                                       \
+        if (split) {                                                                           \
+            hipLaunchKernelGGL((gemm_kernel<WT, E, true>), grid, dim3(256), 0, s, a);          \
+            hipLaunchKernelGGL((gemm_reduce_kernel<E>), dim3(rblocks), dim3(256), 0, s, a);    \
+        } else {                                                                               \
+            hipLaunchKernelGGL((gemm_kernel<WT, E, false>), grid, dim3(256), 0, s, a);         \
+        }                                                                                      \
+    } while (0)
     if (bf16) {
         if (epi == kGemmQkv) ITTS_GEMM(uint16_t, kGemmQkv);
         else if (epi == kGemmResid) ITTS_GEMM(uint16_t, kGemmResid);

@@ -134,8 +134,9 @@ hipError_t launch_step_serialized(const StepArgs& a, int nseq, int grid, bool bf
 // with hipMalloc as prefixes get longer) from this file-scope device array instead, so the
 // call allocates nothing.  Layout for M <= kNoAllocRows prefix rows, every part 256-B aligned:
 //   x, xn, q, att [kNoAllocRows][1280] f32; ff [kNoAllocRows][5120] f32;
-//   row_slot, row_pos [kNoAllocRows] u32; last_rows [64] u32.
-// Each GPU holds its own copy (20 MiB) until the process ends.  Host code never passes the
+//   row_slot, row_pos [kNoAllocRows] u32; last_rows [64] u32; the split-K GEMM workspace
+//   (kGemmWsFloats f32).
+// Each GPU holds its own copy (28 MiB) until the process ends.  Host code never passes the
 // array's name to a kernel: it is a host-side stand-in there.  The device address, per
 // device, comes from hipGetSymbolAddress at decoder creation (scratch_address below).
 constexpr uint32_t kNoAllocRows = 512;
@@ -148,9 +149,10 @@ constexpr size_t kScratchOffFf = kScratchOffAtt + kScratchActBytes;
 constexpr size_t kScratchOffSlot = kScratchOffFf + size_t(kNoAllocRows) * kFfn * 4;
 constexpr size_t kScratchOffPos = kScratchOffSlot + size_t(kNoAllocRows) * 4;
 constexpr size_t kScratchOffLast = kScratchOffPos + size_t(kNoAllocRows) * 4;
-constexpr size_t kScratchBytes = kScratchOffLast + 64 * 4;
+constexpr size_t kScratchOffWs = kScratchOffLast + 64 * 4;
+constexpr size_t kScratchBytes = kScratchOffWs + kGemmWsFloats * 4;
 static_assert(kScratchOffXn % 256 == 0 && kScratchOffFf % 256 == 0 && kScratchOffSlot % 256 == 0 &&
-                  kScratchOffPos % 256 == 0 && kScratchOffLast % 256 == 0 && kMaxBatch <= 64,
+                  kScratchOffPos % 256 == 0 && kScratchOffLast % 256 == 0 && kScratchOffWs % 256 == 0 && kMaxBatch <= 64,
               "scratch parts must stay 256-B aligned");
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
@@ -188,6 +190,7 @@ ScratchEntry* scratch_entry(int dev) {
 struct PrefillBufs {
     float *x, *xn, *q, *att, *ff;
     uint32_t *row_slot, *row_pos, *last_rows;
+    float* ws;  // split-K workspace, kGemmWsFloats
 };
 
 struct Engine {
@@ -215,7 +218,7 @@ struct Engine {
     DevBuf<uint32_t> seg_ids;   // the segments' wrapped text ids
     DevBuf<double> probs;
     // prefill scratch
-    DevBuf<float> px, pxn, pq, patt, pff;
+    DevBuf<float> px, pxn, pq, patt, pff, pws;
     DevBuf<uint32_t> row_slot, row_pos, last_rows;
     // beam search scratch
     DevBuf<float> beam_scores, all_scores;
@@ -705,6 +708,7 @@ struct Engine {
         row_slot.ensure(M);
         row_pos.ensure(M);
         last_rows.ensure(kMaxBatch);
+        pws.ensure(kGemmWsFloats);
         std::vector<uint32_t> slot(M), pos(M), last(kMaxBatch, 0);
         uint32_t m = 0;
         for (int b = 0; b < nseq; ++b) {
@@ -724,7 +728,7 @@ struct Engine {
         HIP_CHECK(hipMemcpyAsync(last_rows.p, last.data(), kMaxBatch * 4, hipMemcpyHostToDevice, stream));
         // Host vectors above must outlive the async copies.
         HIP_CHECK(hipStreamSynchronize(stream));
-        enqueue_prefill_layers(PrefillBufs{px.p, pxn.p, pq.p, patt.p, pff.p, row_slot.p, row_pos.p, last_rows.p}, nseq, M);
+        enqueue_prefill_layers(PrefillBufs{px.p, pxn.p, pq.p, patt.p, pff.p, row_slot.p, row_pos.p, last_rows.p, pws.p}, nseq, M);
     }
 
     // The prefill forward over M stacked rows whose inputs are in b.x, with each row's
@@ -742,6 +746,8 @@ struct Engine {
             g.M = static_cast<int>(M);
             g.N = kQkv;
             g.K = kWidth;
+            g.splits = gemm_splits(static_cast<int>(M), kQkv, kWidth);
+            g.ws = b.ws;
             g.c = pq_;
             g.kv = kv.p;
             g.kv_slot_stride = kv_slot_stride;
@@ -770,6 +776,8 @@ struct Engine {
             p.M = static_cast<int>(M);
             p.N = kWidth;
             p.K = kWidth;
+            p.splits = gemm_splits(static_cast<int>(M), kWidth, kWidth);
+            p.ws = b.ws;
             p.c = px_;
             HIP_CHECK(launch_gemm(p, kGemmResid, bf16, stream));
             HIP_CHECK(launch_ln_rows(LnRowsArgs{px_, pxn_, par + kParLn2W, par + kParLn2B, static_cast<int>(M)}, stream));
@@ -780,6 +788,8 @@ struct Engine {
             f.M = static_cast<int>(M);
             f.N = kFfn;
             f.K = kWidth;
+            f.splits = gemm_splits(static_cast<int>(M), kFfn, kWidth);
+            f.ws = b.ws;
             f.c = pff_;
             HIP_CHECK(launch_gemm(f, kGemmGelu, bf16, stream));
             GemmArgs f2{};
@@ -789,6 +799,8 @@ struct Engine {
             f2.M = static_cast<int>(M);
             f2.N = kWidth;
             f2.K = kFfn;
+            f2.splits = gemm_splits(static_cast<int>(M), kWidth, kFfn);
+            f2.ws = b.ws;
             f2.c = px_;
             HIP_CHECK(launch_gemm(f2, kGemmResid, bf16, stream));
         }
@@ -969,7 +981,8 @@ struct Engine {
         const PrefillBufs b{reinterpret_cast<float*>(base + kScratchOffX),      reinterpret_cast<float*>(base + kScratchOffXn),
                             reinterpret_cast<float*>(base + kScratchOffQ),      reinterpret_cast<float*>(base + kScratchOffAtt),
                             reinterpret_cast<float*>(base + kScratchOffFf),     reinterpret_cast<uint32_t*>(base + kScratchOffSlot),
-                            reinterpret_cast<uint32_t*>(base + kScratchOffPos), reinterpret_cast<uint32_t*>(base + kScratchOffLast)};
+                            reinterpret_cast<uint32_t*>(base + kScratchOffPos), reinterpret_cast<uint32_t*>(base + kScratchOffLast),
+                            reinterpret_cast<float*>(base + kScratchOffWs)};
         struct Flag {  // cleared on every exit, errors included
             bool& f;
             explicit Flag(bool& x) : f(x) { f = true; }
@@ -1210,6 +1223,51 @@ struct Engine {
 
     // Device-to-device copy of 256 MiB of the weight slab (a plain copy kernel of known
     // size, the reference point for HBM traffic counters): bytes = read + written.
+    // Phases of the persistent batch-1 step at `cached_rows` cached rows, from the kernel's own
+    // clock stamps (100 MHz): T_k(l) = the latest workgroup's end of phase k of layer l; the
+    // phase's share of the step is T_k - T_{k-1} (T_0 = the latest layer start).  out[0] mean
+    // layer time, out[1..6] mean phase shares (c_attn, attention tiles, merge, attn.c_proj,
+    // mlp.c_fc, mlp.c_proj), out[7] the head (ln_f, final_norm, mel_head), all in us.
+    void step_phases(uint32_t cached_rows, int iters, float* out) {
+        if (!layers || iters < 1 || !persistent(1, false)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
+        if (!cached_rows) cached_rows = 752;
+        if (cached_rows + 1 >= cap) throw std::invalid_argument("Invalid kernel benchmark request");
+        itts_gen_options o;
+        itts_gen_options_default(&o);
+        SeqState st = make_state(o, cached_rows, 2);
+        st.token = 1;
+        st.position = 2;
+        pinned_state[0] = st;
+        upload_states(1);
+        const size_t per = static_cast<size_t>(layers + 1) * kStepStampsPerLayer;
+        DevBuf<uint64_t> stamps;
+        stamps.alloc(static_cast<size_t>(step_grid) * per);
+        std::vector<uint64_t> host(stamps.n);
+        std::vector<double> sum(8, 0.0);
+        for (int it = 0; it <= iters; ++it) {  // launch 0 warms up
+            HIP_CHECK(hipMemsetAsync(stamps.p, 0, stamps.n * 8, stream));
+            StepArgs a = step_args(0, 1);
+            a.stamps = stamps.p;
+            HIP_CHECK(launch_step_serialized(a, 1, step_grid, bf16, step_dev, stream));
+            HIP_CHECK(hipMemcpyAsync(host.data(), stamps.p, stamps.n * 8, hipMemcpyDeviceToHost, stream));
+            HIP_CHECK(hipStreamSynchronize(stream));
+            check_step_error();
+            if (it == 0) continue;
+            auto T = [&](int l, int k) {
+                uint64_t m = 0;
+                for (int b = 0; b < step_grid; ++b) m = std::max(m, host[b * per + static_cast<size_t>(l) * kStepStampsPerLayer + k]);
+                return static_cast<double>(m);
+            };
+            for (int l = 0; l < layers; ++l) {
+                sum[0] += T(l, 6) - T(l, 0);
+                for (int k = 1; k <= 6; ++k) sum[k] += T(l, k) - T(l, k - 1);
+            }
+            sum[7] += T(layers, 6) - T(layers, 0);
+        }
+        for (int k = 0; k < 7; ++k) out[k] = static_cast<float>(sum[k] / (static_cast<double>(iters) * layers) * 0.01);  // 10 ns ticks
+        out[7] = static_cast<float>(sum[7] / iters * 0.01);
+    }
+
     void bench_copy(int iters, float* avg_ms, double* bytes) {
         const size_t n = std::min<size_t>(slab.n, size_t(256) << 20);
         DevBuf<uint8_t> dst;
@@ -1712,6 +1770,13 @@ int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t c
                           double* bytes_per_launch) {
     return guarded(h, [&] {
         h->e.bench_kernel(which, static_cast<int>(batch), cached_rows, static_cast<int>(iters), avg_ms, bytes_per_launch);
+    });
+}
+
+int itts_gpt_step_phases(itts_gpt* h, uint32_t cached_rows, uint32_t iters, float* phase_us) {
+    return guarded(h, [&] {
+        if (!phase_us) throw std::invalid_argument("Invalid kernel benchmark request");
+        h->e.step_phases(cached_rows, static_cast<int>(iters), phase_us);
     });
 }
 

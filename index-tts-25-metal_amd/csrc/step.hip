@@ -388,11 +388,17 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
     const uint32_t e0 = a.epoch;
     auto ep = [&](int l, uint32_t kind) { return e0 + 8u * static_cast<uint32_t>(l) + kind; };
     const uint32_t n = P.n;
+    // phase-end clocks for measurement (one lane, only when the host asks for them)
+    auto stamp = [&](int l, int k) {
+        if (a.stamps && opaque_tid() == 0)
+            a.stamps[(static_cast<size_t>(P.b) * (a.layers + 1) + l) * kStepStampsPerLayer + k] = __builtin_amdgcn_s_memrealtime();
+    };
 
     for (int l = 0; l < a.layers; ++l) {
         const float* __restrict__ par = a.params + static_cast<size_t>(l) * kParLayer;
         const size_t kvl = static_cast<size_t>(l) * a.kv_layer_stride;
         const int cb = l * P.layer_chunks;  // first chunk of this layer
+        stamp(l, 0);
 
         // ------------------------------------------------ LN1 + c_attn (+ K/V append)
         {
@@ -448,6 +454,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             gemv_rows(ctl, ring, cb, P.qn, x, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
             stores_done();
         }
+        stamp(l, 1);
 
         // ------------------------------------------------ split-KV attention tiles
         {
@@ -572,6 +579,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             release_to(ctl, cb + P.o_proj, wave);
             stores_done();
         }
+        stamp(l, 2);
 
         // ------------------------------------------------ merge of the splits of head h (workgroup h)
         // In attention_merge_kernel's order (decode.hip): its wave w takes splits w, w+4, ...
@@ -667,6 +675,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             }
             cbar(ctl, gen, a.err, failed);  // mpart aliases xs, written below
         }
+        stamp(l, 3);
 
         // ------------------------------------------------ attn.c_proj + residual
         {
@@ -701,6 +710,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             release_to(ctl, cb + P.o_fc, wave);
             stores_done();
         }
+        stamp(l, 4);
 
         // ------------------------------------------------ LN2 + c_fc + GELU
         {
@@ -740,6 +750,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             release_to(ctl, cb + P.o_fc2, wave);
             stores_done();
         }
+        stamp(l, 5);
 
         // ------------------------------------------------ mlp.c_proj + residual -> next h
         {
@@ -775,7 +786,9 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             stores_done();
             // xs and mraw are next written after the next layer's first barrier
         }
+        stamp(l, 6);
     }
+    stamp(a.layers, 0);
 
     // ---------------------------------------------------- ln_f, final_norm, mel_head
     {
@@ -822,6 +835,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
         gemv_rows(ctl, ring, chd, P.hn, x, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
         release_to(ctl, total_chunks, wave);
     }
+    stamp(a.layers, 6);
 }
 
 }  // namespace

@@ -21,6 +21,8 @@
 //   * a second small kernel merges the splits of each head with the usual rescaling
 //     exp(m_s - M) and writes out = sum(w v) / sum(w); the kernel boundary orders the
 //     two passes, so no workgroup needs a device-scope fence or atomic.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace itts {
@@ -33,11 +35,41 @@ __device__ __forceinline__ int live_splits(int L, int max_splits) {
     return min(max_splits, max(1, (L + kAttnSplitRows - 1) / kAttnSplitRows));
 }
 
+// The prologue of a batched GEMV, once per sequence: xn[b] = LayerNorm(s) of sequence b's
+// input row (kProEmbedLn: of h = mel_emb[token] + mel_pos[position], also written to h_out).
+// ln_block<1, 5> is the batch-1 prologue's own reduction, so xn[b] holds exactly the values
+// gemv_kernel<.., B = 1, ..> forms in its registers.  (One small launch per LayerNorm measured
+// faster than forming the B LayerNorms in every workgroup of the batched GEMV.)
+template <int PRO>
+__global__ __launch_bounds__(256) void ln_seq_kernel(GemvArgs a) {
+    const int b = blockIdx.x, tid = threadIdx.x;
+    __shared__ float red[4];
+    float v[1][5];
+    if constexpr (PRO == kProEmbedLn) {
+        const bool live = b < a.nseq;
+        const uint32_t tok = live ? a.state[b].token : 0u, pos = live ? a.state[b].position : 0u;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int c = tid + 256 * i;
+            v[0][i] = a.mel_emb[static_cast<size_t>(tok) * kWidth + c] + a.mel_pos[static_cast<size_t>(pos) * kWidth + c];
+            a.h_out[b * kWidth + c] = v[0][i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) v[0][i] = a.x[b * a.x_stride + tid + 256 * i];
+    }
+    ln_block<1, 5>(v, a.ln_w, a.ln_b, red);
+    if constexpr (PRO == kProLn2) ln_block<1, 5>(v, a.ln2_w, a.ln2_b, red);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) a.xn[b * kWidth + tid + 256 * i] = v[0][i];
+}
+
 template <int COLS, int RPW, int B, typename WT, int PRO, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     constexpr int J = COLS / 256;  // 16-byte chunks per lane per row
     constexpr int PER = kWidth / 256;
-    static_assert(PRO == kProNone || COLS == kWidth, "LayerNorm prologue is 1280 wide");
+    static_assert(PRO == kProNone || PRO == kProStaged || COLS == kWidth, "LayerNorm prologue is 1280 wide");
+    constexpr bool STAGED = PRO == kProStaged;
     using LD = WLoad<WT>;
     using VT = typename LD::vec;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -67,6 +99,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
     }
 
+    // Staged input: its first 1280 columns requested before the weights too (loads complete in
+    // order, so a later request would wait for the whole weight fetch).  16-byte pieces: piece
+    // f < B * 320 is columns 4 (f % 320) .. of sequence f / 320.
+    // (5120-wide rows, whose four chunks would otherwise hold too many registers at once: 4-byte
+    // pieces, thread t taking columns t + 256 i of each sequence)
+    constexpr bool WIDE = COLS > kWidth;
+    constexpr int XF = kWidth / 4;                  // 16-byte pieces per sequence and chunk
+    constexpr int NX = WIDE ? B * PER : (B * XF + 255) / 256;  // pieces per thread
+    using XP = typename std::conditional<WIDE, float, float4>::type;
+    XP xr[STAGED ? NX : 1];
+    auto x_piece = [&](int q, int i) -> XP {       // piece tid + 256 i of chunk q
+        const int f = tid + 256 * i;
+        if constexpr (WIDE) {  // i = b * PER + k: column tid + 256 k of sequence b
+            return a.x[(i / PER) * a.x_stride + q * kWidth + tid + 256 * (i % PER)];
+        } else {
+            return f < B * XF ? *reinterpret_cast<const float4*>(a.x + (f / XF) * a.x_stride + q * kWidth + (f % XF) * 4)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    if constexpr (STAGED) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i) xr[i] = x_piece(0, i);
+    }
+
     const WT* __restrict__ w = static_cast<const WT*>(a.w);
     VT wv[RPW][J];
 #pragma unroll
@@ -77,9 +133,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         for (int j = 0; j < J; ++j) wv[r][j] = LD::load(w, static_cast<size_t>(rr) * (COLS / 4) + j * 64 + lane);
     }
 
-    __shared__ float xs[PRO == kProNone ? 4 : B * kWidth];
+    __shared__ float xs[PRO == kProNone ? 4 : (STAGED && COLS > kWidth ? 2 : 1) * B * kWidth];
     __shared__ float red[B * kNW];
-    if constexpr (PRO != kProNone) {
+    if constexpr (PRO != kProNone && !STAGED) {
         if constexpr (PRO == kProEmbedLn) {
             if (blockIdx.x == 0) {
 #pragma unroll
@@ -102,8 +158,52 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+    if constexpr (STAGED) {
+        // x through LDS, 1280 columns at a time (two buffers when there are several chunks):
+        // chunk q + 1 is loaded into registers while chunk q's FMAs run.  Per (row, sequence)
+        // the FMA chain runs over j in order, as below.
+        constexpr int NCH = COLS / kWidth;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
+        for (int q = 0; q < NCH; ++q) {
+            float* xq = xs + (q & 1) * B * kWidth;
+#pragma unroll
+            for (int i = 0; i < NX; ++i) {
+                const int f = tid + 256 * i;
+                if (WIDE || f < B * XF) {
+                    if constexpr (WIDE) {
+                        xq[(i / PER) * kWidth + tid + 256 * (i % PER)] = xr[i];
+                    } else {
+                        *reinterpret_cast<float4*>(xq + (f / XF) * kWidth + (f % XF) * 4) = xr[i];
+                    }
+                }
+            }
+            __syncthreads();
+            if (q + 1 < NCH) {
+#pragma unroll
+                for (int i = 0; i < NX; ++i) xr[i] = x_piece(q + 1, i);
+            }
+#pragma unroll
+            for (int jj = 0; jj < kWidth / 256; ++jj) {
+                const int j = q * (kWidth / 256) + jj;
+                float4 xv[B];
+#pragma unroll
+                for (int b = 0; b < B; ++b) xv[b] = *reinterpret_cast<const float4*>(xq + b * kWidth + (jj * 64 + lane) * 4);
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float4 w4 = LD::to_f4(wv[r][j]);
+#pragma unroll
+                    for (int b = 0; b < B; ++b) {
+                        acc[r][b] = __builtin_fmaf(w4.x, xv[b].x, acc[r][b]);
+                        acc[r][b] = __builtin_fmaf(w4.y, xv[b].y, acc[r][b]);
+                        acc[r][b] = __builtin_fmaf(w4.z, xv[b].z, acc[r][b]);
+                        acc[r][b] = __builtin_fmaf(w4.w, xv[b].w, acc[r][b]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < (STAGED ? 0 : J); ++j) {
         float4 xv[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -186,14 +286,34 @@ hipError_t launch_gemv(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
 
 // ------------------------------------------------------------------ attention
 
+// One (sequence b, head h, split s) tile of the split pass.
+__device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, int s, int L, int S);
+
+// The grid is a fixed kAttnGrid workgroups (a captured graph replays it whatever the cache
+// lengths are); they walk this step's live tiles t = blockIdx.x, blockIdx.x + gridDim.x, ...
+// in the order (sequence, split, head), so no workgroup is launched for a split beyond a
+// sequence's live ones.
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    if (b >= a.nseq) return;
-    const SeqState& st = a.state[b];
-    if (!st.active) return;
-    const int L = static_cast<int>(st.n) + 1;  // cached rows + the row appended by this step
-    const int S = live_splits(L, a.splits);
-    if (s >= S) return;
+    int off[kMaxBatch + 1];  // first tile of each sequence
+    int Ls[kMaxBatch];
+    off[0] = 0;
+#pragma unroll
+    for (int b = 0; b < kMaxBatch; ++b) {
+        const bool live = b < a.nseq && a.state[b].active;
+        Ls[b] = live ? static_cast<int>(a.state[b].n) + 1 : 0;  // cached rows + the row appended by this step
+        off[b + 1] = off[b] + (live ? kHeads * live_splits(Ls[b], a.splits) : 0);
+    }
+    for (int t = blockIdx.x; t < off[kMaxBatch]; t += gridDim.x) {
+        int b = 0;
+#pragma unroll
+        for (int q = 1; q < kMaxBatch; ++q) b += t >= off[q] ? 1 : 0;
+        const int r = t - off[b];
+        attention_tile(a, b, r % kHeads, r / kHeads, Ls[b], live_splits(Ls[b], a.splits));
+        __syncthreads();  // the tile's LDS (redm, reds, accs) is reused by the next one
+    }
+}
+
+__device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, int s, int L, int S) {
     const int chunk = (L + S - 1) / S;
     const int p0 = s * chunk;
     const int p1 = min(L, p0 + chunk);
@@ -316,26 +436,60 @@ int gemv_batch_bucket(int batch) {
     return -1;
 }
 
+// Batches of 2 or more: the LayerNorm'd inputs are formed once (ln_seq_kernel), and the
+// GEMV reads them (or its plain input) through LDS (kProStaged).  At batch 1 the GEMV forms
+// the LayerNorm itself, with the same reduction, so every batch size gives the same bits.
+template <int PRO>
+hipError_t launch_ln_seq(const GemvArgs& a, int batch, hipStream_t s) {
+    if (!a.xn) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((ln_seq_kernel<PRO>), dim3(gemv_batch_bucket(batch)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+GemvArgs staged_on_xn(const GemvArgs& a) {
+    GemvArgs b = a;
+    b.x = a.xn;
+    b.x_stride = kWidth;
+    return b;
+}
+
 // Rows per wave: chosen so every launch has >= 320 workgroups of 4 waves.
 hipError_t launch_gemv_qkv(const GemvArgs& a, int batch, bool bf16, bool embed, hipStream_t s) {
+    if (batch >= 2) {
+        const hipError_t e = embed ? launch_ln_seq<kProEmbedLn>(a, batch, s) : launch_ln_seq<kProLn>(a, batch, s);
+        if (e != hipSuccess) return e;
+        return launch_gemv<kWidth, 2, kProStaged, kEpiQkv>(staged_on_xn(a), batch, bf16, s);
+    }
     return embed ? launch_gemv<kWidth, 2, kProEmbedLn, kEpiQkv>(a, batch, bf16, s)
                  : launch_gemv<kWidth, 2, kProLn, kEpiQkv>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_proj(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    if (batch >= 2) return launch_gemv<kWidth, 1, kProStaged, kEpiResid>(a, batch, bf16, s);
     return launch_gemv<kWidth, 1, kProNone, kEpiResid>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_fc(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    if (batch >= 2) {
+        const hipError_t e = launch_ln_seq<kProLn>(a, batch, s);
+        if (e != hipSuccess) return e;
+        return launch_gemv<kWidth, 2, kProStaged, kEpiGelu>(staged_on_xn(a), batch, bf16, s);
+    }
     return launch_gemv<kWidth, 2, kProLn, kEpiGelu>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_fc2(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    if (batch >= 2) return launch_gemv<kFfn, 1, kProStaged, kEpiResid>(a, batch, bf16, s);
     return launch_gemv<kFfn, 1, kProNone, kEpiResid>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_head(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
+    if (batch >= 2) {
+        const hipError_t e = launch_ln_seq<kProLn2>(a, batch, s);
+        if (e != hipSuccess) return e;
+        return launch_gemv<kWidth, 2, kProStaged, kEpiLogits>(staged_on_xn(a), batch, bf16, s);
+    }
     return launch_gemv<kWidth, 2, kProLn2, kEpiLogits>(a, batch, bf16, s);
 }
 
 hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s) {
-    hipLaunchKernelGGL(attention_kernel, dim3(a.splits, kHeads, batch), dim3(256), 0, s, a);
+    if (a.nseq > kMaxBatch) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attention_kernel, dim3(std::min(kAttnGrid, a.splits * kHeads * batch)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(attention_merge_kernel, dim3(kHeads, batch), dim3(256), 0, s, a);
     return hipGetLastError();
 }

@@ -12,6 +12,7 @@ enum Prologue : int {
     kProLn = 1,       // x = LayerNorm(x_in)
     kProEmbedLn = 2,  // h = mel_emb[token] + mel_pos[position] (written out), x = LayerNorm(h)
     kProLn2 = 3,      // x = LayerNorm_b(LayerNorm_a(x_in)) (ln_f then final_norm)
+    kProStaged = 4,   // x read from global as is, through LDS in 1280-column chunks (batches)
 };
 enum Epilogue : int {
     kEpiQkv = 0,     // q row / K,V cache append at row n
@@ -46,6 +47,9 @@ struct GemvArgs {
     float* h_out;           // [batch][1280]
     const SeqState* state;  // [batch]
     int nseq;               // sequences with state entries (<= batch template)
+    // batches of 2 or more: the LayerNorm'd input rows [batch][1280], formed once per launch
+    // by a small kernel instead of in every GEMV workgroup
+    float* xn;
 };
 
 // Batch templates instantiated for the decode GEMVs; the runtime pads a batch up
@@ -77,7 +81,9 @@ struct AttnArgs {
 constexpr int kAttnMaxChunk = 128;   // rows per split at most
 constexpr int kAttnSplitRows = 64;   // target rows per split
 constexpr int kAttnMaxSplits = 64;   // splits per (sequence, head) at most
-// Split pass (grid splits x 20 x batch) then merge pass (grid 20 x batch).
+// Split pass (kAttnGrid workgroups walking the live (sequence, split, head) tiles) then
+// merge pass (grid 20 x batch).
+constexpr int kAttnGrid = 1024;
 hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 
 // ------------------------------------------------------------------ persistent decode step

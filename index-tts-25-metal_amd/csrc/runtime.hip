@@ -211,6 +211,7 @@ struct Engine {
     DevBuf<float> kv;
     size_t kv_slot_stride = 0, kv_layer_stride = 0, kv_v_off = 0;
     DevBuf<float> h, hmid, q, attn, ff, logits, partial;
+    DevBuf<float> xn;  // LayerNorm'd GEMV inputs of a batched step, [kMaxBatch][1280]
     DevBuf<uint32_t> codes, status, d_parent;
     DevBuf<SeqState> state;  // kMaxBatch + 1 entries; the last one serves the processor/sampler API
     DevBuf<uint8_t> seen, seen_tmp, table, table_tmp;
@@ -429,6 +430,7 @@ struct Engine {
         q.alloc(B * kWidth);
         attn.alloc(B * kWidth);
         ff.alloc(B * kFfn);
+        xn.alloc(B * kWidth);
         // Enough splits that no split exceeds kAttnMaxChunk rows at full capacity.
         splits = std::max<int>((cap + kAttnSplitRows - 1) / kAttnSplitRows, (cap + kAttnMaxChunk - 1) / kAttnMaxChunk);
         splits = std::min(splits, kAttnMaxSplits);
@@ -548,6 +550,7 @@ struct Engine {
         a.kv_slot_stride = kv_slot_stride;
         a.kv_v_off = kv_v_off;
         a.kv_cap = cap;
+        a.xn = xn.p;
         return a;
     }
 

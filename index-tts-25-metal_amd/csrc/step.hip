@@ -367,7 +367,10 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
     if (!st.active) return;
     if (tid < kLW) ctl.done[tid] = 0;
     if (tid < kCW) ctl.need[tid] = 0;
-    if (tid == 0) ctl.bar = 0;
+    if (tid == 0) {
+        ctl.bar = 0;
+        ctl.go = 0;
+    }
     __syncthreads();  // the only barrier of the whole workgroup; roles split below
 
     Plan P;
@@ -375,10 +378,24 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
     const int total_chunks = a.layers * P.layer_chunks + P.hn;
 
     // ================================================================ loaders
+    // They start once the compute waves hold layer 0's input row: requested first, those
+    // loads do not queue behind the whole grid's first weight chunks (which held layer 0's
+    // start back by 6-10 us).
     if (wave >= kCW) {
+        wait_go(ctl, a.err);
         run_loader(a, P, ring, ctl, __builtin_amdgcn_readfirstlane(wave - kCW), lane);
         return;
     }
+
+    // h = mel_emb[token] + mel_pos[position] (gpt.cpp:79-85, kernels.metal:1310-1324)
+    float h0[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const int c = tid + 256 * i;
+        h0[i] = a.mel_emb[static_cast<size_t>(st.token) * kWidth + c] + a.mel_pos[static_cast<size_t>(st.position) * kWidth + c];
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    if (tid == 0) lds_st(&ctl.go, 1u);
 
     // ================================================================ compute waves
     bool failed = false;
@@ -420,12 +437,8 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             bias.load(par + kParQkvB + P.q0, P.qn, wave, lane);
             float hv[5];
             if (l == 0) {
-                // h = mel_emb[token] + mel_pos[position] (gpt.cpp:79-85, kernels.metal:1310-1324)
 #pragma unroll
-                for (int i = 0; i < 5; ++i) {
-                    const int c = tid + 256 * i;
-                    hv[i] = a.mel_emb[static_cast<size_t>(st.token) * kWidth + c] + a.mel_pos[static_cast<size_t>(st.position) * kWidth + c];
-                }
+                for (int i = 0; i < 5; ++i) hv[i] = h0[i];
             } else {
                 xr.wait(XB, idx, ep(l, kEpXh), hv, a.err, failed);
             }

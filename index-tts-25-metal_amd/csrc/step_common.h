@@ -136,7 +136,20 @@ struct alignas(16) Ctl {
     uint32_t done[kLW];  // loader w: 1 + last chunk index landed (its chunks are w, w+4, ...)
     uint32_t need[kCW];  // compute wave c: first chunk it may still read
     uint32_t bar;        // compute-wave barrier arrivals
+    uint32_t go;         // step.hip: set once layer 0's input row has arrived; loaders start then
 };
+
+// A loader wave's wait for ctl.go (bounded like every wait of the step kernels).
+__device__ __forceinline__ void wait_go(Ctl& ctl, uint32_t* err) {
+    unsigned spins = 0;
+    while (lds_ld(&ctl.go) == 0) {
+        if (++spins > kLdsSpinLimit) {
+            atomicOr(err, 1u);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
 
 // Barrier of the 4 compute waves (the loader waves never join it).
 __device__ __forceinline__ void cbar(Ctl& ctl, uint32_t& gen, uint32_t* err, bool& failed) {
@@ -154,46 +167,7 @@ __device__ __forceinline__ void cbar(Ctl& ctl, uint32_t& gen, uint32_t* err, boo
     }
 }
 
-__device__ __forceinline__ float lane_value(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
-
-// A 1280-wide row in LDS, as the 256 threads of ln_block<1, 5> (common.h) hold it:
-// v[w][i] = row[64 w + lane + 256 i], i.e. thread 64 w + lane's five values.
-__device__ __forceinline__ void ln_layout_load(const float* row, int lane, float (&v)[4][5]) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-#pragma unroll
-        for (int i = 0; i < 5; ++i) v[w][i] = row[64 * w + lane + 256 * i];
-}
-
-// Mean and 1 / sqrt(var + eps) of that row in ln_block<1, 5>'s order (each thread sums its
-// five values, each wave reduces its threads by butterfly, the four wave sums are added in
-// order), computed by one wave for all four: wave_sum4 reduces the four waves' values with
-// wave_sum's pairings, so every compute wave gets the statistics without a barrier.
-__device__ __forceinline__ void ln_stats(const float (&v)[4][5], float& mean, float& inv) {
-    float s[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        s[w] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 5; ++i) s[w] += v[w][i];
-    }
-    float r = wave_sum4(s[0], s[1], s[2], s[3]);  // waves 0, 1, 2, 3 in lanes 0, 32, 16, 48
-    mean = (((lane_value(r, 0) + lane_value(r, 32)) + lane_value(r, 16)) + lane_value(r, 48)) / float(kWidth);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        s[w] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const float d = v[w][i] - mean;
-            s[w] += d * d;
-        }
-    }
-    r = wave_sum4(s[0], s[1], s[2], s[3]);
-    const float var = (((lane_value(r, 0) + lane_value(r, 32)) + lane_value(r, 16)) + lane_value(r, 48)) / float(kWidth);
-    inv = 1.0f / sqrtf(var + kLnEps);
-}
-// ln_block's per-element step
-__device__ __forceinline__ float ln_apply(float v, float mean, float inv, float g, float b) { return (v - mean) * inv * g + b; }
+// lane_value, ln_layout_load, ln_stats and ln_apply live in common.h.
 
 // gamma/beta of this thread's 5 LayerNorm columns (tid + 256 i), loaded ahead of the input.
 struct LnPar {

@@ -330,7 +330,8 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
             }
             if (t == 0) {
                 *a.rng = rng;
-                // Stable sort by score, descending (std::sort on <= 16 candidates is an insertion sort).
+                // Stable sort by score, descending: the reference is built with libc++, whose std::sort
+                // keeps equal candidates in order below 24 elements (take <= 20).
                 for (int x = 1; x < take; ++x) {
                     const uint32_t v = ids[x];
                     int y = x - 1;
@@ -411,7 +412,8 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
         }
         if (t == 0) {
             *a.rng = rng;
-            // Stable sort by score, descending (std::sort on <= 16 candidates is an insertion sort).
+            // Stable sort by score, descending: the reference is built with libc++, whose std::sort
+            // keeps equal candidates in order below 24 elements (take <= 20).
             for (int x = 1; x < take; ++x) {
                 const uint32_t v = ids[x];
                 int y = x - 1;

@@ -307,14 +307,23 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
     const float mx = sm.mx;
     double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : P_global;
     for (uint32_t j = t; j < m; j += NT) P[j] = libm::exp_glibc(static_cast<double>(sm.s[sm.list[j]] - mx));
-    // Keys: (score key << 32) | j; j increases with the index, so ties break by index.
+    // Keys: (score key << 32) | (j << 1) | negative-zero flag.  j increases with the index, so
+    // ties break by index; -0 and +0 share the key of +0, since the reference's comparator
+    // (gpt_sampling.cpp:78-83) finds them equal, and the flag (below j, so it never decides
+    // the order) brings back the sign when the scores are rebuilt.
     int n = 64;
     while (n < static_cast<int>(m)) n <<= 1;
     uint64_t keys[kSortMax / NT];
 #pragma unroll
     for (int q = 0; q < kSortMax / NT; ++q) {
         const int j = t + q * NT;
-        keys[q] = j < static_cast<int>(m) ? (static_cast<uint64_t>(float_key(sm.s[sm.list[j]])) << 32) | static_cast<uint32_t>(j) : ~0ull;
+        if (j < static_cast<int>(m)) {
+            const float v = sm.s[sm.list[j]];
+            const uint32_t nz = __float_as_uint(v) == 0x80000000u ? 1u : 0u;
+            keys[q] = (static_cast<uint64_t>(float_key(nz ? 0.0f : v)) << 32) | (static_cast<uint32_t>(j) << 1) | nz;
+        } else {
+            keys[q] = ~0ull;
+        }
     }
     __syncthreads();  // s[] is overwritten by the sort buffer below
 #pragma unroll
@@ -342,7 +351,7 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
             double cumulative = 0.0;
             for (uint32_t c0 = 0; c0 < m; c0 += 64) {
                 const uint32_t q = c0 + lane;
-                const uint32_t j = q < m ? static_cast<uint32_t>(sm.sortbuf[q]) : 0u;
+                const uint32_t j = q < m ? static_cast<uint32_t>(sm.sortbuf[q]) >> 1 : 0u;
                 const double r = q < m ? P[j] / total : 0.0;
                 const int cn = static_cast<int>(min(64u, m - c0));
                 uint64_t removed = 0;
@@ -355,7 +364,7 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
             const uint32_t keep = min(m, beams > 1 ? 2u : 1u);
             if (static_cast<uint32_t>(lane) < keep) {
                 const uint32_t q = m - keep + lane;
-                sm.list[static_cast<uint32_t>(sm.sortbuf[q])] &= ~kRemoved;
+                sm.list[static_cast<uint32_t>(sm.sortbuf[q]) >> 1] &= ~kRemoved;
             }
         }
     }
@@ -375,9 +384,9 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
     for (int q = 0; q < kSortMax / NT; ++q) {
         const uint64_t k = keys[q];
         if (k == ~0ull) continue;
-        const uint32_t j = static_cast<uint32_t>(k);
+        const uint32_t j = static_cast<uint32_t>(k) >> 1;
         const uint16_t e = sm.list[j];
-        if (!(e & kRemoved)) sm.s[e & 0x7fff] = key_float(static_cast<uint32_t>(k >> 32));
+        if (!(e & kRemoved)) sm.s[e & 0x7fff] = (k & 1u) ? -0.0f : key_float(static_cast<uint32_t>(k >> 32));
     }
     __syncthreads();
     return kOk;

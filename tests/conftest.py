@@ -41,6 +41,12 @@ def full_weights(itts):
     return itts.make_synthetic_weights(layers=24, seed=0)
 
 
+def same_bits(a, b) -> bool:
+    """Float32 arrays equal bit for bit (so -0.0 and +0.0 differ, unlike ==)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def rel_err(a: np.ndarray, b: np.ndarray) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

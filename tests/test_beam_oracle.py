@@ -40,6 +40,31 @@ def test_beam_search_returns_exhaustive_best(oracle, case):
     assert got == (list(codes), eos), (got, codes, eos)
 
 
+def test_planted_mistakes_change_the_exhaustive_answer(oracle):
+    """The enumeration is discriminating: with a planted mistake (the length penalty dropped, or
+    the processors run without the hypothesis' own history) its best hypothesis differs from the
+    correct one in some cases, and in each of them the oracle's search returns the correct one,
+    not the mistaken one."""
+    mistakes = {
+        "no length penalty": lambda proc, lpen: (proc, 0.0),
+        "processors without history": lambda proc, lpen: (lambda lp, h: proc(lp, [1, 8192]), lpen),
+    }
+    for name, plant in mistakes.items():
+        caught = 0
+        for case, (good, opts, beams, steps) in enumerate(bb.CASES):
+            tokens, _, _ = bb.case_tokens(good)
+            proc = _processors(oracle, opts)
+            (_, codes, eos), _ = bb.best(bb.head_bias(good), proc, opts["length_penalty"], steps, tokens)
+            wrong_proc, wrong_lpen = plant(proc, opts["length_penalty"])
+            (_, wcodes, weos), _ = bb.best(bb.head_bias(good), wrong_proc, wrong_lpen, steps, tokens)
+            if (wcodes, weos) == (codes, eos):
+                continue
+            got = _model(oracle, good).generate(np.zeros((3, 128), np.float32), oracle.options(num_beams=beams, **opts), steps)
+            assert got == (list(codes), eos) and got != (list(wcodes), weos), (name, case)
+            caught += 1
+        assert caught > 0, name
+
+
 def test_initial_beam_scores_minus_1e9_closed_form(oracle):
     """Three beams, two steps, penalty 10, length penalty 0; the head leaves token a = 17 and the
     stop token as the only good candidates, with log-probabilities la > le (about -0.43 and

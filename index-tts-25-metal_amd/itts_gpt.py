@@ -655,6 +655,34 @@ def make_synthetic_codec_weights(seed: int = 0, std: float = 0.02) -> Dict[str, 
     return out
 
 
+QWEN_VOCAB, QWEN_WIDTH, QWEN_Q, QWEN_KV, QWEN_FFN, QWEN_LAYERS, QWEN_EOS = 151936, 1024, 2048, 1024, 3072, 28, 151643
+
+
+def qwen_weight_shapes(layers: int = QWEN_LAYERS) -> Dict[str, tuple]:
+    """The tensors QwenDecoder reads (src/qwen.cpp:5-15, 23-45), reference names."""
+    s = {"qwen.model.embed_tokens.weight": (QWEN_VOCAB, QWEN_WIDTH), "qwen.model.norm.weight": (QWEN_WIDTH,)}
+    for i in range(layers):
+        p = f"qwen.model.layers.{i}"
+        s.update({f"{p}.self_attn.q_proj.weight": (QWEN_Q, QWEN_WIDTH), f"{p}.self_attn.k_proj.weight": (QWEN_KV, QWEN_WIDTH),
+                  f"{p}.self_attn.v_proj.weight": (QWEN_KV, QWEN_WIDTH), f"{p}.self_attn.o_proj.weight": (QWEN_WIDTH, QWEN_Q),
+                  f"{p}.self_attn.q_norm.weight": (128,), f"{p}.self_attn.k_norm.weight": (128,),
+                  f"{p}.mlp.gate_proj.weight": (QWEN_FFN, QWEN_WIDTH), f"{p}.mlp.up_proj.weight": (QWEN_FFN, QWEN_WIDTH),
+                  f"{p}.mlp.down_proj.weight": (QWEN_WIDTH, QWEN_FFN), f"{p}.input_layernorm.weight": (QWEN_WIDTH,),
+                  f"{p}.post_attention_layernorm.weight": (QWEN_WIDTH,)})
+    return s
+
+
+def make_synthetic_qwen_weights(layers: int = QWEN_LAYERS, seed: int = 0, std: float = 0.02) -> Dict[str, np.ndarray]:
+    """Random-init Qwen3-0.6B decoder weights: matrices and the embedding N(0, std^2), RMSNorm
+    weights N(1, 0.1^2)."""
+    out: Dict[str, np.ndarray] = {}
+    for name, shape in qwen_weight_shapes(layers).items():
+        n, key = int(np.prod(shape)), _tensor_seed(seed, name)
+        v = synthetic_normal(n, key, 1.0, 0.1) if len(shape) == 1 else synthetic_normal(n, key, 0.0, std)
+        out[name] = v.reshape(shape)
+    return out
+
+
 class EnhancedCodec:
     """The decode path of itts25::EnhancedCodec (include/itts25/codec.hpp:11-17) on the MI355X."""
 

@@ -54,6 +54,9 @@ struct Snapshot {
 
 }  // namespace
 
+// The thread's last error message, shared with the Qwen oracle (qwen_oracle.cpp).
+std::string& orc_error_message() { return g_err; }
+
 struct orc_model {
     uint32_t width = 0, heads = 0, ffn = 0, layers = 0, cap = 0;
     uint32_t text_vocab = 0, lang_vocab = 0, text_pos_rows = 0, mel_pos_rows = 0;

@@ -65,6 +65,14 @@ def _load() -> C.CDLL:
         "orc_libm_eval": (None, [C.c_int32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_void_p]),
         "orc_layernorm": (None, [f32p, f32p, f32p, u32, C.c_float, f32p]),
         "orc_last_error": (C.c_char_p, []),
+        "orc_qwen_create": (P, [C.POINTER(_T), C.c_int32, u32, C.c_char_p, C.c_size_t]),
+        "orc_qwen_destroy": (None, [P]),
+        "orc_qwen_cached": (u32, [P]),
+        "orc_qwen_prefill": (C.c_int, [P, u32p, u32, f32p]),
+        "orc_qwen_step": (C.c_int, [P, u32, f32p]),
+        "orc_qwen_generate": (C.c_int, [P, u32p, u32, u32, u32p, u32p]),
+        "orc_qwen_kv_row": (C.c_int, [P, u32, C.c_int32, u32, f32p]),
+        "orc_qwen_set_mutation": (None, [P, C.c_int32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -191,6 +199,67 @@ class OracleGpt:
         _check(_lib.orc_generate(self._h, _fp(p), p.size // self.width, C.byref(opt), max_tokens, _up(codes), C.byref(n),
                                  C.byref(stopped)))
         return [int(c) for c in codes[: n.value]], bool(stopped.value)
+
+
+QWEN_VOCAB = 151936
+QWEN_EOS = 151643
+
+
+class OracleQwen:
+    """FP32 CPU restatement of itts25::QwenDecoder (src/qwen.cpp:5-49); see qwen_oracle.h."""
+
+    def __init__(self, weights: Dict[str, np.ndarray], layers: int = 28):
+        ts = []
+        for name, a in weights.items():
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            shape = (C.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
+            ts.append((_T(name.encode(), a.ctypes.data, shape, a.ndim, 0), a))
+        arr = (_T * len(ts))(*[t for t, _ in ts])
+        err = C.create_string_buffer(512)
+        self._h = _lib.orc_qwen_create(arr, len(ts), layers, err, 512)  # copies the tensors
+        if not self._h:
+            raise OracleError(-2, err.value.decode())
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.orc_qwen_destroy(self._h)
+            self._h = None
+
+    @property
+    def cached(self) -> int:
+        return int(_lib.orc_qwen_cached(self._h))
+
+    def set_mutation(self, mutation: int) -> None:
+        _lib.orc_qwen_set_mutation(self._h, int(mutation))
+
+    def prefill(self, ids: Sequence[int]) -> np.ndarray:
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(QWEN_VOCAB, np.float32)
+        _check(_lib.orc_qwen_prefill(self._h, _up(a), a.size, _fp(out)))
+        return out
+
+    def step(self, token: int) -> np.ndarray:
+        out = np.empty(QWEN_VOCAB, np.float32)
+        _check(_lib.orc_qwen_step(self._h, int(token) & 0xFFFFFFFF, _fp(out)))
+        return out
+
+    def generate(self, ids: Sequence[int], maximum: int = 1024) -> Tuple[List[int], bool]:
+        """(tokens, reached EOS): the tokens produced also when the reference would throw
+        "Qwen did not reach EOS within 1024 generated tokens"."""
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.zeros(max(1, maximum), np.uint32)
+        n = C.c_uint32(0)
+        st = _lib.orc_qwen_generate(self._h, _up(a), a.size, int(maximum) & 0xFFFFFFFF, _up(out), C.byref(n))
+        toks = [int(x) for x in out[: n.value]]
+        if st == -2 and _lib.orc_last_error().decode() == "Qwen did not reach EOS within 1024 generated tokens":
+            return toks, False
+        _check(st)
+        return toks, True
+
+    def kv_row(self, layer: int, is_v: bool, pos: int) -> np.ndarray:
+        out = np.empty(1024, np.float32)
+        _check(_lib.orc_qwen_kv_row(self._h, layer, int(is_v), pos, _fp(out)))
+        return out
 
 
 def processors(logits: np.ndarray, history: Sequence[int], opt: _O) -> np.ndarray:

@@ -37,7 +37,7 @@ DEVICE_FLAGS = [
     f"-I{CSRC}",
 ]
 SOURCES = ["decode.hip", "step.hip", "step_batch.hip", "sampler.hip", "beam.hip", "prefill.hip", "util.hip", "runtime.hip",
-           "codec.hip", "libm_check.hip"]
+           "codec.hip", "libm_check.hip", "qwen.hip"]
 HOST_SOURCES = ["bundle.cpp"]  # host-only C++ (g++)
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"]
 

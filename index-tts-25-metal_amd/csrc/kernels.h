@@ -208,7 +208,9 @@ struct LnRowsArgs {
 };
 hipError_t launch_ln_rows(const LnRowsArgs& a, hipStream_t s);
 
-enum GemmEpi : int { kGemmQkv = 0, kGemmResid = 1, kGemmGelu = 2 };
+// kGemmStore: c[M][N] = dot + bias.  kGemmSwiglu: output columns come in (gate, up) pairs
+// 2i, 2i + 1; c[M][N / 2] gets silu(gate) * up (the Qwen MLP with interleaved weight rows).
+enum GemmEpi : int { kGemmQkv = 0, kGemmResid = 1, kGemmGelu = 2, kGemmStore = 3, kGemmSwiglu = 4 };
 struct GemmArgs {
     const float* a;         // [M][K]
     const void* w;          // [N][K] fp32 or bf16

@@ -53,10 +53,15 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, int row, int col, 
     } else if constexpr (EPI == kGemmResid) {
         float* p = a.c + static_cast<size_t>(row) * a.N + col;
         *p = *p + v;
+    } else if constexpr (EPI == kGemmStore) {
+        a.c[static_cast<size_t>(row) * a.N + col] = v;
     } else {
         a.c[static_cast<size_t>(row) * a.N + col] = gelu_f(v);
     }
 }
+
+// SiLU-gated product of one (gate, up) column pair (kernels.metal:363-374).
+__device__ __forceinline__ float swiglu_f(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
 // SPLIT: this workgroup covers K range [z Kz, (z + 1) Kz) of split z = blockIdx.z and
 // writes its raw partial tile to a.ws[z][M][N]; gemm_reduce_kernel finishes it.
@@ -124,6 +129,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             const int row = m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
             if (row < a.M) ws[static_cast<size_t>(row) * a.N + col] = acc[i];
         }
+    } else if constexpr (EPI == kGemmSwiglu) {
+        // columns col and col ^ 1 sit in lanes l and l ^ 1, on the same rows
+        const float bias = a.bias[col];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            const float v = acc[i] + bias;
+            const float u = __shfl_xor(v, 1, 64);
+            if (row < a.M && !(col & 1)) a.c[static_cast<size_t>(row) * (a.N / 2) + col / 2] = swiglu_f(v, u);
+        }
     } else {
         const float bias = a.bias[col];
 #pragma unroll
@@ -139,6 +154,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a) {
     const size_t total = static_cast<size_t>(a.M) * a.N, plane = total;
+    if constexpr (EPI == kGemmSwiglu) {  // one thread per (gate, up) column pair
+        for (size_t e2 = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; e2 < total / 2;
+             e2 += static_cast<size_t>(gridDim.x) * blockDim.x) {
+            const size_t e = 2 * e2;
+            float g = a.ws[e], u = a.ws[e + 1];
+            for (int z = 1; z < a.splits; ++z) {
+                g += a.ws[z * plane + e];
+                u += a.ws[z * plane + e + 1];
+            }
+            const int col = static_cast<int>(e % a.N);
+            a.c[e2] = swiglu_f(g + a.bias[col], u + a.bias[col + 1]);
+        }
+        return;
+    }
     for (size_t e = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += static_cast<size_t>(gridDim.x) * blockDim.x) {
         float d = a.ws[e];
         for (int z = 1; z < a.splits; ++z) d += a.ws[z * plane + e];
@@ -226,7 +255,11 @@ hipError_t launch_gemm(const GemmArgs& a, int epi, bool bf16, hipStream_t s) {
             hipLaunchKernelGGL((gemm_kernel<WT, E, false>), grid, dim3(256), 0, s, a);         \
         }                                                                                      \
     } while (0)
-    if (bf16) {
+    if (epi == kGemmStore || epi == kGemmSwiglu) {  // FP32 weights only (the Qwen decoder)
+        if (bf16) return hipErrorInvalidValue;
+        if (epi == kGemmStore) ITTS_GEMM(float, kGemmStore);
+        else ITTS_GEMM(float, kGemmSwiglu);
+    } else if (bf16) {
         if (epi == kGemmQkv) ITTS_GEMM(uint16_t, kGemmQkv);
         else if (epi == kGemmResid) ITTS_GEMM(uint16_t, kGemmResid);
         else ITTS_GEMM(uint16_t, kGemmGelu);

@@ -23,7 +23,7 @@ import os
 import zlib
 from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -75,6 +75,10 @@ class _Timing(C.Structure):
     _fields_ = [("prefill_ms", C.c_float), ("decode_ms", C.c_float), ("decode_steps", C.c_uint32), ("decode_path", C.c_uint32)]
 
 
+class _QwenConfig(C.Structure):
+    _fields_ = [("layers", C.c_uint32), ("flags", C.c_uint32)]
+
+
 def _load() -> C.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(f"HIP extension not built: {LIB_PATH} is missing (run index-tts-25-metal_amd/build.py)")
@@ -122,6 +126,15 @@ def _load() -> C.CDLL:
         "itts_codec_decode": (C.c_int, [P, u32p, u32, f32p]),
         "itts_codec_bench": (C.c_int, [P, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
         "itts_libm_eval": (C.c_int, [i32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_void_p]),
+        "itts_qwen_create": (C.c_int, [C.POINTER(_Tensor), i32, C.POINTER(_QwenConfig), C.POINTER(P)]),
+        "itts_qwen_create_from_bundle": (C.c_int, [P, C.POINTER(_QwenConfig), C.POINTER(P)]),
+        "itts_qwen_destroy": (None, [P]),
+        "itts_qwen_last_error": (C.c_char_p, [P]),
+        "itts_qwen_prefill": (C.c_int, [P, u32p, u32, f32p]),
+        "itts_qwen_step": (C.c_int, [P, u32, f32p]),
+        "itts_qwen_generate": (C.c_int, [P, u32p, u32, u32, u32p, u32p]),
+        "itts_qwen_submissions": (C.c_uint64, [P]),
+        "itts_qwen_bench": (C.c_int, [P, u32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -742,3 +755,83 @@ def synthetic_prefix_inputs(n_text: int, seed: int, n_cond: int = 32, text_vocab
     rng = np.random.default_rng(seed)
     text = rng.integers(0, text_vocab, size=n_text, dtype=np.int64).astype(np.uint32)
     return cond, text
+
+
+QWEN_DID_NOT_STOP = "Qwen did not reach EOS within 1024 generated tokens"
+
+
+class QwenDecoder:
+    """itts25::QwenDecoder (include/itts25/qwen.hpp:5-18, src/qwen.cpp:5-49) on the MI355X."""
+
+    def __init__(self, weights: Dict[str, np.ndarray], layers: int = QWEN_LAYERS):
+        keep, table = {}, []
+        for name, v in weights.items():
+            a = keep[name] = np.ascontiguousarray(v, dtype=np.float32)
+            shape = (C.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
+            table.append(_Tensor(name.encode(), a.ctypes.data, shape, a.ndim, 0))
+        arr = (_Tensor * max(1, len(table)))(*table)
+        self._q = C.c_void_p()
+        st = _lib.itts_qwen_create(arr, len(table), C.byref(_QwenConfig(layers, 0)), C.byref(self._q))
+        if st != 0:
+            _raise(st, _lib.itts_qwen_last_error(None).decode())
+
+    @classmethod
+    def from_bundle(cls, bundle: "Bundle", layers: int = QWEN_LAYERS) -> "QwenDecoder":
+        self = cls.__new__(cls)
+        self._q = C.c_void_p()
+        st = _lib.itts_qwen_create_from_bundle(bundle._b, C.byref(_QwenConfig(layers, 0)), C.byref(self._q))
+        if st != 0:
+            _raise(st, _lib.itts_qwen_last_error(None).decode())
+        return self
+
+    def close(self) -> None:
+        if getattr(self, "_q", None):
+            _lib.itts_qwen_destroy(self._q)
+            self._q = None
+
+    def __del__(self):
+        if _lib is not None:
+            self.close()
+
+    def _check(self, st: int) -> None:
+        if st != 0:
+            _raise(st, _lib.itts_qwen_last_error(self._q).decode())
+
+    def prefill(self, ids: Sequence[int]) -> np.ndarray:
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(QWEN_VOCAB, np.float32)
+        self._check(_lib.itts_qwen_prefill(self._q, _up(a), a.size, _fp(out)))
+        return out
+
+    def step(self, token: int) -> np.ndarray:
+        out = np.empty(QWEN_VOCAB, np.float32)
+        self._check(_lib.itts_qwen_step(self._q, int(token) & 0xFFFFFFFF, _fp(out)))
+        return out
+
+    def generate_tokens(self, ids: Sequence[int], maximum: int = 1024) -> Tuple[List[int], bool]:
+        """(ids, reached EOS): the ids produced also when generate() raises at `maximum`."""
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.zeros(max(1, int(maximum)), np.uint32)
+        n = C.c_uint32(0)
+        st = _lib.itts_qwen_generate(self._q, _up(a), a.size, int(maximum) & 0xFFFFFFFF, _up(out), C.byref(n))
+        toks = [int(x) for x in out[: n.value]]
+        if st == -2 and _lib.itts_qwen_last_error(self._q).decode() == QWEN_DID_NOT_STOP:
+            return toks, False
+        self._check(st)
+        return toks, True
+
+    def generate(self, ids: Sequence[int], maximum: int = 1024) -> List[int]:
+        """QwenDecoder::generate (qwen.cpp:46-49): greedy ids up to and including EOS."""
+        toks, eos = self.generate_tokens(ids, maximum)
+        if not eos:
+            raise GptRuntimeError(QWEN_DID_NOT_STOP)
+        return toks
+
+    def submissions(self) -> int:
+        return int(_lib.itts_qwen_submissions(self._q))
+
+    def bench(self, prompt: int, cached_rows: int, iters: int) -> Tuple[float, float]:
+        """(prefill ms of `prompt` ids, mean µs per decode step from `cached_rows` rows)."""
+        pm, su = C.c_float(0), C.c_float(0)
+        self._check(_lib.itts_qwen_bench(self._q, prompt, cached_rows, iters, C.byref(pm), C.byref(su)))
+        return pm.value, su.value

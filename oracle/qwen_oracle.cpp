@@ -218,7 +218,7 @@ orc_qwen* orc_qwen_create(const orc_tensor* tensors, int32_t count, uint32_t lay
             auto it = by.find(name);
             if (it == by.end()) throw std::runtime_error("Missing tensor: " + name);
             const orc_tensor* t = it->second;
-            if (std::vector<int64_t>(t->shape, t->shape + t->ndim) != shape) throw std::runtime_error("Unsupported Qwen shape: " + name);
+            if (std::vector<int64_t>(t->shape, t->shape + t->ndim) != shape) throw std::invalid_argument("Unsupported Qwen shape: " + name);
             size_t n = 1;
             for (int64_t s : shape) n *= static_cast<size_t>(s);
             return std::vector<float>(t->data, t->data + n);

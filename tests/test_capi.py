@@ -1,4 +1,4 @@
-"""The C-ABI library loads and exports every entry point include/itts_gpt.h declares (CPU only:
+"""The C-ABI library loads and exports every entry point include/*.h declares (CPU only:
 no compute call is made)."""
 import ctypes
 import re
@@ -10,7 +10,7 @@ ROOT = Path(__file__).resolve().parent.parent
 
 
 def declared_symbols():
-    text = (ROOT / "include" / "itts_gpt.h").read_text()
+    text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     return sorted(set(re.findall(r"\b(itts_\w+)\s*\(", text)))
 
 

@@ -116,6 +116,35 @@ def batch8_inputs(it, dec):
     return prefixes, opts
 
 
+QWEN_WEIGHT_BYTES = 28 * 15_728_640 * 4 + 151_936 * 1024 * 4 + (28 * 2304 + 1024) * 4  # slab, tied embedding, norms
+QWEN_KV_BYTES_PER_ROW = 28 * 2 * 8 * 128 * 4                                        # K and V of one row, all layers
+
+
+def qwen_step_bytes(rows: int) -> float:
+    """Algorithmic HBM bytes of one Qwen decode step with `rows` cache rows after it: every
+    weight byte once, the cache rows' K and V, the 151936 logits written."""
+    return QWEN_WEIGHT_BYTES + QWEN_KV_BYTES_PER_ROW * rows + 151_936 * 4
+
+
+def qwen_workload(it):
+    """The Qwen3-0.6B emotion-text decoder (src/qwen.cpp), 28 layers, synthetic weights: a
+    64-id prompt, greedy generation of 256 ids (random weights reach no EOS, so every call runs
+    to the maximum), whole-call tokens/s; prefill time and the decode step's HIP-event time at
+    64 + 128 cache rows."""
+    q = it.QwenDecoder(it.make_synthetic_qwen_weights(seed=1))
+    prompt = [int(x) for x in np.random.default_rng(12).integers(0, 151936, 64)]
+    q.generate_tokens(prompt, 32)
+    r, times = timed(lambda: q.generate_tokens(prompt, 256), 2)
+    prefill_ms, step_us = q.bench(64, 64 + 128, 100)
+    q.close()
+    rows = 64 + 128 + 50  # the mean cache length over the 100 timed steps, plus the new row
+    gbs = qwen_step_bytes(rows) / (step_us * 1e-6) / 1e9
+    return {"prompt": 64, "generated": len(r[0]), "reached_eos": r[1], "seconds": round(min(times), 4),
+            "tokens_per_s": round(len(r[0]) / min(times), 2), "prefill_ms_64": round(prefill_ms, 3),
+            "step_us_at_192_rows": round(step_us, 2), "step_algorithmic_GBps": round(gbs, 1),
+            "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def extras(it, dec, weights):
     """Beam-3, long-context, 8-segment request and batch-8 (FP32, BF16) workloads of the same model."""
     res = {}
@@ -205,6 +234,7 @@ def extras(it, dec, weights):
             got = d.prefill(prefixes[0])
             res["batch8_bf16"]["prefill_logit_maxabs_vs_f32"] = float(np.max(np.abs(got - ref)))
             d.close()
+    res["qwen3_emotion_decoder"] = qwen_workload(it)
     return res
 
 
@@ -219,7 +249,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--kernel-only", default=None, help="time one kernel kind only (for profiler runs); 'codec': a 600-code codec decode; 'beam3': the beam-3 workload; "
                          "'batch8' / 'batch8_bf16': the 8-sequence workload; "
-                         "'prefill': the 155-row prefill")
+                         "'prefill': the 155-row prefill; 'qwen': the Qwen3 emotion-text decoder")
     ap.add_argument("--iters", type=int, default=240)
     ap.add_argument("--kernel-batch", type=int, default=1, help="sequences per launch for --kernel-only")
     args = ap.parse_args()
@@ -269,6 +299,11 @@ def main() -> int:
                           "decode_tokens_per_s": round(8 * (tm["decode_steps"] - 1) / (tm["decode_ms"] * 1e-3), 2),
                           "ms_per_step": round(tm["decode_ms"] / max(1, tm["decode_steps"] - 1), 4),
                           "prefill_ms": round(tm["prefill_ms"], 3)}), flush=True)
+        return 0
+    if args.kernel_only == "qwen":
+        # the extras' Qwen workload alone (64-id prompt, 256 greedy ids, 28 layers), for profilers
+        dec.close()
+        print(json.dumps({"kernel": "qwen", **qwen_workload(it)}), flush=True)
         return 0
     if args.kernel_only == "codec":
         codec = it.EnhancedCodec(it.make_synthetic_codec_weights(seed=0))

@@ -80,7 +80,7 @@ def build_shim() -> Path:
     _run([
         "g++", "-O2", "-std=c++17", "-Wall",
         f"-I{cpp}", f"-I{INCLUDE}",
-        str(cpp / "gpt.cpp"), str(cpp / "codec.cpp"), str(cpp / "gpt_shim_example.cpp"),
+        str(cpp / "gpt.cpp"), str(cpp / "codec.cpp"), str(cpp / "qwen.cpp"), str(cpp / "gpt_shim_example.cpp"),
         f"-L{PKG}", "-litts_gpt", f"-Wl,-rpath,{PKG}",
         "-o", str(tmp),
     ])

@@ -3,7 +3,9 @@
 // a device-context object, prepare -> generate.  `gpt_shim_example run` uses a synthetic
 // weight table; `gpt_shim_example bundle <dir>` loads a MIT2 bundle through itts25::BundleWeights;
 // both execute on the GPU.  Without arguments it only checks that the shim links.
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -13,6 +15,7 @@
 
 #include "itts25/codec.hpp"
 #include "itts25/gpt.hpp"
+#include "itts25/qwen.hpp"
 
 namespace {
 struct TensorInfo {
@@ -71,6 +74,60 @@ int run_bundle_with(W& w) {
     return 0;
 }
 
+// `gpt_shim_example qwen|qwenref|qwentable <dir> <prompt ids...>`: QwenDecoder the way
+// src/main.cpp:160-166 drives it (prefill, three steps, generate), from BundleWeights, from a
+// reference-style Weights (bundle().root()), or from a plain info()/get() table filled from
+// the bundle.  Prints the prefill's argmax and logit sum, the steps' argmaxes, the generated
+// ids, the failure of a generate that stops one id short of EOS, and the submissions.
+template <class W>
+int run_qwen_with(W& w, const std::vector<uint32_t>& prompt) {
+    itts25::QwenDecoder qwen(w);
+    const auto logits = qwen.prefill(prompt);
+    auto argmax = [](const std::vector<float>& x) { return static_cast<long>(std::max_element(x.begin(), x.end()) - x.begin()); };
+    double sum = 0;
+    for (float v : logits) sum += v;
+    std::printf("{\"prefill_argmax\":%ld,\"prefill_sum\":%.9g,\"steps\":[", argmax(logits), sum);
+    for (uint32_t i = 1; i <= 3; ++i) std::printf("%s%ld", i > 1 ? "," : "", argmax(qwen.step(prompt[i % prompt.size()])));
+    const auto ids = qwen.generate(prompt, 12);
+    std::printf("],\"generated\":[");
+    for (size_t i = 0; i < ids.size(); ++i) std::printf("%s%u", i ? "," : "", ids[i]);
+    std::string short_error = "none";
+    try {
+        qwen.generate(prompt, static_cast<uint32_t>(ids.size() - 1));
+    } catch (const std::runtime_error& e) {
+        short_error = e.what();
+    }
+    std::printf("],\"short_error\":\"%s\",\"submissions\":%llu}\n", short_error.c_str(),
+                static_cast<unsigned long long>(qwen.submissions()));
+    return 0;
+}
+
+int run_qwen(const char* mode, const char* path, const std::vector<uint32_t>& prompt) {
+    if (std::strcmp(mode, "qwenref") == 0) {
+        RefStyleWeights w(path);
+        return run_qwen_with(w, prompt);
+    }
+    itts25::BundleWeights b(path);
+    if (std::strcmp(mode, "qwen") == 0) return run_qwen_with(b, prompt);
+    TableWeights t;  // info()/get() only
+    {
+        std::vector<std::string> names{"qwen.model.embed_tokens.weight", "qwen.model.norm.weight"};
+        for (unsigned l = 0; l < ITTS_QWEN_LAYERS; ++l) {
+            const std::string p = "qwen.model.layers." + std::to_string(l);
+            for (const char* s : {".self_attn.q_proj.weight", ".self_attn.k_proj.weight", ".self_attn.v_proj.weight",
+                                  ".self_attn.o_proj.weight", ".self_attn.q_norm.weight", ".self_attn.k_norm.weight",
+                                  ".mlp.gate_proj.weight", ".mlp.up_proj.weight", ".mlp.down_proj.weight",
+                                  ".input_layernorm.weight", ".post_attention_layernorm.weight"})
+                names.push_back(p + s);
+        }
+        for (const auto& n : names) {
+            t.infos[n] = {b.info(n).shape};
+            t.data[n] = b.get(n);
+        }
+    }
+    return run_qwen_with(t, prompt);
+}
+
 int run_bundle(const char* path, bool ref_style) {
     if (ref_style) {
         RefStyleWeights w(path);
@@ -83,6 +140,11 @@ int run_bundle(const char* path, bool ref_style) {
 int main(int argc, char** argv) {
     if (argc >= 3 && std::strcmp(argv[1], "bundle") == 0) return run_bundle(argv[2], false);
     if (argc >= 3 && std::strcmp(argv[1], "refbundle") == 0) return run_bundle(argv[2], true);
+    if (argc >= 4 && std::strncmp(argv[1], "qwen", 4) == 0) {
+        std::vector<uint32_t> prompt;
+        for (int i = 3; i < argc; ++i) prompt.push_back(static_cast<uint32_t>(std::strtoul(argv[i], nullptr, 10)));
+        return run_qwen(argv[1], argv[2], prompt);
+    }
     if (argc < 2 || std::strcmp(argv[1], "run") != 0) {
         std::printf("gpt shim linked\n");
         return 0;

@@ -1,10 +1,12 @@
-"""The C++ drop-in stays a drop-in: the reference's own callers of itts25::GptDecoder and
-itts25::EnhancedCodec compile against index-tts-25-metal_amd/cpp (CPU only).
+"""The C++ drop-in stays a drop-in: the reference's own callers of itts25::GptDecoder,
+itts25::EnhancedCodec and itts25::QwenDecoder compile against index-tts-25-metal_amd/cpp (CPU
+only).
 
-Callers (src/pipeline.cpp:12-25, src/native_runtime.cpp:98-100, src/server.cpp:41-47,
-src/main.cpp:31-66) are syntax-checked with g++ -std=c++17 -fsyntax-only, with this
-repository's cpp/ ahead of the reference's include/ on the search path, so "itts25/gpt.hpp"
-and "itts25/codec.hpp" resolve to the drop-in and every other header to the reference's own.
+Callers (src/pipeline.cpp:12-25, src/native_runtime.cpp:50-53, 98-100, src/server.cpp:33-47,
+src/main.cpp:31-66, 159-169) are syntax-checked with g++ -std=c++17 -fsyntax-only, with this
+repository's cpp/ ahead of the reference's include/ on the search path, so "itts25/gpt.hpp",
+"itts25/codec.hpp" and "itts25/qwen.hpp" resolve to the drop-in and every other header to the
+reference's own.
 Runs only where the reference tree is present (it is read, not built or copied).
 """
 import shutil
@@ -34,5 +36,8 @@ def test_reference_caller_compiles_against_dropin(caller):
     included = [ln.lstrip(". ").strip() for ln in p.stderr.splitlines() if ln.startswith(".")]
     gpt = [h for h in included if h.endswith("itts25/gpt.hpp")]
     assert gpt and all(Path(h).resolve().is_relative_to(CPP) for h in gpt), gpt
-    codec = [h for h in included if h.endswith("itts25/codec.hpp")]
-    assert all(Path(h).resolve().is_relative_to(CPP) for h in codec), codec
+    for name in ("itts25/codec.hpp", "itts25/qwen.hpp"):
+        hs = [h for h in included if h.endswith(name)]
+        assert all(Path(h).resolve().is_relative_to(CPP) for h in hs), hs
+    if caller in ("main", "native_runtime", "server"):  # the QwenDecoder callers
+        assert any(h.endswith("itts25/qwen.hpp") for h in included), caller

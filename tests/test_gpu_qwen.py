@@ -105,10 +105,16 @@ def relabel(w, a, b):
 
 def test_generate_stops_at_eos(itts, oracle, qw, pair):
     dec, orc = pair
-    prompt = ids_of(11, 12)
-    toks, _ = orc.generate(prompt, 12)
-    k = next(i for i in range(1, len(toks)) if toks[i] not in toks[:i] and toks[i] not in prompt)
-    w2 = relabel(qw, toks[k], itts.QWEN_EOS)
+    for seed in range(11, 40):  # a prompt whose greedy ids are not one repeated id
+        prompt = ids_of(seed, 12)
+        toks, _ = orc.generate(prompt, 12)
+        ks = [i for i in range(1, len(toks)) if toks[i] not in toks[:i]]
+        if ks:
+            break
+    k, t = ks[0], toks[ks[0]]
+    assert itts.QWEN_EOS not in prompt + toks
+    prompt = [itts.QWEN_EOS if x == t else x for x in prompt]  # t and EOS swap names everywhere
+    w2 = relabel(qw, t, itts.QWEN_EOS)
     d2 = itts.QwenDecoder(w2, layers=LAYERS)
     assert d2.generate(prompt, 12) == toks[:k] + [itts.QWEN_EOS]
     assert d2.generate_tokens(prompt, k + 1) == (toks[:k] + [itts.QWEN_EOS], True)

@@ -15,9 +15,9 @@
 //     contiguous, so a decode-attention tile is one contiguous range per K and per V.
 // Decode (one token): per layer
 //   q_gemv<RMSNorm, store>  (the layer-0 one gathers the embedding row of the state's token)
-//   q_prep_kernel           per-head RMSNorm of q and k, RoPE, K/V rows into the cache
-//   q_attn_kernel           split-KV attention, 64 rows x one KV head per tile, both query
-//                           heads of the KV head, partial (max, sum, weighted V) per split
+//   q_attn_kernel           per-head RMSNorm of q and k and RoPE, the step's K/V row into the
+//                           cache, then split-KV attention, 64 rows x one KV head per tile,
+//                           both query heads of the KV head, partial (max, sum, weighted V)
 //   q_attn_merge_kernel     the splits merged with exp(m_s - M) rescaling
 //   q_gemv<-, residual>     o_proj, added to the residual stream in place
 //   q_gemv<RMSNorm, swiglu> gate/up pairs -> silu(gate) * up
@@ -102,12 +102,15 @@ struct QPrepArgs {
 };
 
 struct QAttnArgs {
-    const float* q;        // [2048]
-    const float* kc;
-    const float* vc;
+    const float* qkv;      // the step row's raw q | k | v [4096]
+    float* kc;             // this layer's K cache [8][kCap][128]
+    float* vc;
+    const float* q_norm;
+    const float* k_norm;
+    const float* inv_freq;
     float* part_acc;       // [kMaxSplits][16][128]
     float* part_ml;        // [kMaxSplits][16][2]: max, sum
-    float* att;            // merge output [2048]
+    float* att;            // [2048] the merged attention output
     const QState* st;
 };
 
@@ -150,6 +153,19 @@ __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+// One head's per-head RMSNorm then RoPE at position pos (qwen.cpp:29-32; qwen_rope,
+// kernels.metal:3111-3115), by one wave: lane l holds dimensions l and l + 64, the pair the
+// rotation mixes.  Returns the two outputs.
+__device__ __forceinline__ float2 head_norm_rope(float x1, float x2, const float* g, const float* inv_freq, uint32_t pos) {
+    const int l = threadIdx.x & 63;
+    const float ss = wave_sum(__builtin_fmaf(x1, x1, x2 * x2));
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHd) + kEps);
+    const float n1 = x1 * inv * g[l], n2 = x2 * inv * g[l + 64];
+    float sn, cs;
+    sincosf(static_cast<float>(pos) * inv_freq[l], &sn, &cs);
+    return make_float2(n1 * cs + (-n2) * sn, n2 * cs + n1 * sn);
+}
 
 // (v, i) replaces (bv, bi) under mit2_gpt_argmax_f32's rule (kernels.metal:1283-1297).
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) { return v > bv || (v == bv && i < bi); }
@@ -330,46 +346,70 @@ __global__ __launch_bounds__(64) void q_prep_kernel(QPrepArgs a) {
     }
     const bool isq = hh < kQH;
     const int col = isq ? hh * kHd : kQ + (hh - kQH) * kHd;
-    const float x1 = src[col + l], x2 = src[col + l + 64];
-    const float* g = isq ? a.q_norm : a.k_norm;
-    const float ss = wave_sum(__builtin_fmaf(x1, x1, x2 * x2));
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHd) + kEps);
-    const float n1 = x1 * inv * g[l], n2 = x2 * inv * g[l + 64];
-    float sn, cs;
-    sincosf(static_cast<float>(pos) * a.inv_freq[l], &sn, &cs);
-    const float o1 = n1 * cs + (-n2) * sn, o2 = n2 * cs + n1 * sn;
+    const float2 o = head_norm_rope(src[col + l], src[col + l + 64], isq ? a.q_norm : a.k_norm, a.inv_freq, pos);
     float* dst = isq ? a.q + static_cast<size_t>(r) * kQ + hh * kHd : a.kc + (static_cast<size_t>(hh - kQH) * kCap + pos) * kHd;
-    dst[l] = o1;
-    dst[l + 64] = o2;
+    dst[l] = o.x;
+    dst[l + 64] = o.y;
 }
 
 // ------------------------------------------------------------------- decode attention
 // Tiles (split, KV head) over a fixed grid (the graph is captured before the length is known):
 // a tile is cache rows [64 s, 64 s + 64) of one KV head against both of its query heads
-// (head / 2 = KV head, kernels.metal:3120).  Eight 32-lane groups take 8 rows each, one float4
-// of the 128 dimensions per lane; K and V rows are loaded up front.  Partial results: the
-// split's max score, its sum of exp(score - max) and its weighted V sum.
+// (head / 2 = KV head, kernels.metal:3120).  Each tile first forms its two query heads from the
+// raw projection (per-head RMSNorm, RoPE at the step's position: waves 0 and 1); the tile that
+// holds the step's own row also forms that row's K (wave 2) and V (wave 3), uses them from LDS
+// and writes them to the cache (kernels.metal:3116-3118).  Eight 32-lane groups take 8 rows
+// each, one float4 of the 128 dimensions per lane, K and V loaded up front.  Partial results:
+// the split's max score, its sum of exp(score - max) and its weighted V sum.
 __global__ __launch_bounds__(256) void q_attn_kernel(QAttnArgs a) {
     if (!a.st->active) return;
-    const int L = static_cast<int>(a.st->cached) + 1;
+    const uint32_t cached = a.st->cached;
+    const int L = static_cast<int>(cached) + 1;
+    const int own = static_cast<int>(cached) / kSplitRows;  // the split holding the step's row
     const int tiles = ((L + kSplitRows - 1) / kSplitRows) * kKVH;
-    const int tid = threadIdx.x, g = tid >> 5, j = tid & 31;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = tid >> 5, j = tid & 31;
+    __shared__ __align__(16) float qs[2][kHd];
+    __shared__ __align__(16) float knew[kHd], vnew[kHd];
     __shared__ float gm[2][8], gl[2][8];
     __shared__ float4 gacc[8][2][32];
     for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
         const int split = t / kKVH, kvh = t % kKVH;
+        float* kb = a.kc + static_cast<size_t>(kvh) * kCap * kHd;
+        float* vb = a.vc + static_cast<size_t>(kvh) * kCap * kHd;
+        if (wave < 2) {
+            const int col = (2 * kvh + wave) * kHd;
+            const float2 o = head_norm_rope(a.qkv[col + lane], a.qkv[col + lane + 64], a.q_norm, a.inv_freq, cached);
+            qs[wave][lane] = o.x;
+            qs[wave][lane + 64] = o.y;
+        } else if (split == own) {
+            if (wave == 2) {
+                const int col = kQ + kvh * kHd;
+                const float2 o = head_norm_rope(a.qkv[col + lane], a.qkv[col + lane + 64], a.k_norm, a.inv_freq, cached);
+                knew[lane] = o.x;
+                knew[lane + 64] = o.y;
+                kb[static_cast<size_t>(cached) * kHd + lane] = o.x;
+                kb[static_cast<size_t>(cached) * kHd + lane + 64] = o.y;
+            } else {
+                const int col = kQ + kKV + kvh * kHd;
+                const float v1 = a.qkv[col + lane], v2 = a.qkv[col + lane + 64];
+                vnew[lane] = v1;
+                vnew[lane + 64] = v2;
+                vb[static_cast<size_t>(cached) * kHd + lane] = v1;
+                vb[static_cast<size_t>(cached) * kHd + lane + 64] = v2;
+            }
+        }
+        __syncthreads();
         const int r0 = split * kSplitRows + g * 8;
-        const float4 q0 = *reinterpret_cast<const float4*>(a.q + (2 * kvh) * kHd + 4 * j);
-        const float4 q1 = *reinterpret_cast<const float4*>(a.q + (2 * kvh + 1) * kHd + 4 * j);
-        const float* kb = a.kc + static_cast<size_t>(kvh) * kCap * kHd;
-        const float* vb = a.vc + static_cast<size_t>(kvh) * kCap * kHd;
+        const float4 q0 = *reinterpret_cast<const float4*>(&qs[0][4 * j]);
+        const float4 q1 = *reinterpret_cast<const float4*>(&qs[1][4 * j]);
         float4 kr[8], vr[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const bool ok = r0 + i < L;
-            const size_t off = static_cast<size_t>(ok ? r0 + i : 0) * kHd + 4 * j;
-            kr[i] = ok ? *reinterpret_cast<const float4*>(kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
-            vr[i] = ok ? *reinterpret_cast<const float4*>(vb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int row = r0 + i;
+            const bool cached_row = row < static_cast<int>(cached);
+            const size_t off = static_cast<size_t>(cached_row ? row : 0) * kHd + 4 * j;
+            kr[i] = cached_row ? *reinterpret_cast<const float4*>(kb + off) : *reinterpret_cast<const float4*>(&knew[4 * j]);
+            vr[i] = cached_row ? *reinterpret_cast<const float4*>(vb + off) : *reinterpret_cast<const float4*>(&vnew[4 * j]);
         }
         float s0[8], s1[8], m0 = -INFINITY, m1 = -INFINITY;
 #pragma unroll
@@ -431,10 +471,11 @@ __global__ __launch_bounds__(256) void q_attn_kernel(QAttnArgs a) {
             a.part_ml[(split * kQH + qh) * 2] = h ? M1 : M0;
             a.part_ml[(split * kQH + qh) * 2 + 1] = l;
         }
-        __syncthreads();  // gm / gl / gacc are reused by the next tile
+        __syncthreads();  // qs / knew / vnew / gm / gl / gacc are reused by the next tile
     }
 }
 
+// The splits of each query head merged with exp(m_s - M) rescaling, in split order.
 __global__ __launch_bounds__(128) void q_attn_merge_kernel(QAttnArgs a) {
     if (!a.st->active) return;
     const int qh = blockIdx.x, d = threadIdx.x;
@@ -571,7 +612,7 @@ struct Engine {
     hipStream_t stream = nullptr;
     hipEvent_t ev[2] = {nullptr, nullptr};
     Buf<float> slab, embed, norms, inv_freq, zeros, kv;
-    Buf<float> h, qkv, q, att, ff, logits, part_acc, part_ml;
+    Buf<float> h, qkv, att, ff, logits, part_acc, part_ml;
     Buf<float2> best;
     Buf<QState> st;
     Buf<uint32_t> toks, ids;
@@ -684,12 +725,11 @@ struct Engine {
         kv.alloc(static_cast<size_t>(layers) * 2 * kKVH * kCap * kHd);
         h.alloc(kD);
         qkv.alloc(kQkvN);
-        q.alloc(kQ);
-        att.alloc(kQ);
         ff.alloc(kF);
         logits.alloc(kV);
         part_acc.alloc(static_cast<size_t>(kMaxSplits) * kQH * kHd);
         part_ml.alloc(static_cast<size_t>(kMaxSplits) * kQH * 2);
+        att.alloc(kQ);
         best.alloc(kHeadBlocks);
         st.alloc(1);
         toks.alloc(kMaxGen);
@@ -793,10 +833,7 @@ struct Engine {
             a.out = qkv.p;
             if (l == 0) gemv<kD, 2, kProEmbedRms, kEpiStore>(a, s);
             else gemv<kD, 2, kProRms, kEpiStore>(a, s);
-            QPrepArgs pa{qkv.p, 1, q.p, K(l), Vc(l), N(l) + kNormQ, N(l) + kNormK, inv_freq.p, st.p};
-            hipLaunchKernelGGL(q_prep_kernel, dim3(1, kQH + 2 * kKVH), dim3(64), 0, s, pa);
-            QWEN_CHECK(hipGetLastError());
-            QAttnArgs aa{q.p, K(l), Vc(l), part_acc.p, part_ml.p, att.p, st.p};
+            QAttnArgs aa{qkv.p, K(l), Vc(l), N(l) + kNormQ, N(l) + kNormK, inv_freq.p, part_acc.p, part_ml.p, att.p, st.p};
             hipLaunchKernelGGL(q_attn_kernel, dim3(kAttnGrid), dim3(256), 0, s, aa);
             QWEN_CHECK(hipGetLastError());
             hipLaunchKernelGGL(q_attn_merge_kernel, dim3(kQH), dim3(kHd), 0, s, aa);

@@ -224,39 +224,43 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
             }
         }
     }
+    // The RPW * B sums, four at a time: wave_sum4(a, b, c, d) leaves sum(a) in lanes 0-15,
+    // sum(c) in 16-31, sum(b) in 32-47 and sum(d) in 48-63, with wave_sum's pairings, so each
+    // sum is bitwise the one wave_sum gives.  Lane L then owns accumulator
+    // i = 4 (L & 15) + {0, 2, 1, 3}[L >> 4] (one (row, sequence) pair per lane, no loop over
+    // the pairs).
+    constexpr int NV = RPW * B, NK = (NV + 3) / 4;
+    auto accv = [&](int i) -> float { return i < NV ? acc[i / B][i % B] : 0.0f; };
+    float red4[NK];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r)
+    for (int k = 0; k < NK; ++k) red4[k] = wave_sum4(accv(4 * k), accv(4 * k + 1), accv(4 * k + 2), accv(4 * k + 3));
+    const int lw = lane & 15, lg = lane >> 4;
+    const int i = 4 * lw + ((lg == 1) ? 2 : (lg == 2) ? 1 : lg);
+    float sum = red4[0];
 #pragma unroll
-        for (int b = 0; b < B; ++b) acc[r][b] = wave_sum(acc[r][b]);
-
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const int row = row0 + r;
-        if (row >= a.rows) continue;
-        const float bias = a.bias[row];
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            if (lane != ((r * B + b) & 63)) continue;
-            const float v = acc[r][b] + bias;
-            if constexpr (EPI == kEpiQkv) {
-                if (row < kWidth) {
-                    a.q[b * kWidth + row] = v;
-                } else if (b < a.nseq && a.state[b].active) {
-                    const int rr = row - kWidth;
-                    const bool is_v = rr >= kWidth;
-                    const int c = is_v ? rr - kWidth : rr;
-                    const size_t off = static_cast<size_t>(b) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
-                                       (static_cast<size_t>(c >> 6) * a.kv_cap + a.state[b].n) * kHeadDim + (c & 63);
-                    a.kv[off] = v;
-                }
-            } else if constexpr (EPI == kEpiResid) {
-                a.out[b * a.out_stride + row] = a.resid[b * a.out_stride + row] + v;
-            } else if constexpr (EPI == kEpiGelu) {
-                a.out[b * a.out_stride + row] = gelu_f(v);
-            } else {
-                a.out[b * a.out_stride + row] = v;
-            }
+    for (int k = 1; k < NK; ++k) sum = lw == k ? red4[k] : sum;
+    if (lw >= NK || i >= NV) return;
+    const int r = i / B, b = i % B;
+    const int row = row0 + r;
+    if (row >= a.rows) return;
+    const float v = sum + a.bias[row];
+    if constexpr (EPI == kEpiQkv) {
+        if (row < kWidth) {
+            a.q[b * kWidth + row] = v;
+        } else if (b < a.nseq && a.state[b].active) {
+            const int rr = row - kWidth;
+            const bool is_v = rr >= kWidth;
+            const int c = is_v ? rr - kWidth : rr;
+            const size_t off = static_cast<size_t>(b) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
+                               (static_cast<size_t>(c >> 6) * a.kv_cap + a.state[b].n) * kHeadDim + (c & 63);
+            a.kv[off] = v;
         }
+    } else if constexpr (EPI == kEpiResid) {
+        a.out[b * a.out_stride + row] = a.resid[b * a.out_stride + row] + v;
+    } else if constexpr (EPI == kEpiGelu) {
+        a.out[b * a.out_stride + row] = gelu_f(v);
+    } else {
+        a.out[b * a.out_stride + row] = v;
     }
 }
 

@@ -86,12 +86,36 @@ constexpr int kAttnMaxSplits = 64;   // splits per (sequence, head) at most
 constexpr int kAttnGrid = 1024;
 hipError_t launch_attention(const AttnArgs& a, int batch, hipStream_t s);
 
+// ------------------------------------------------------------------ sampler
+enum SampleMode : int {
+    kModeDecode = 0,      // processors from state options + seen mask, choose, advance state
+    kModeProcessors = 1,  // processors only, write processed scores to out_scores
+    kModeDraw = 2,        // logits are already processed: draw `draws` tokens with state.rng
+};
+struct SampleArgs {
+    const float* logits;    // [batch][logit_stride]
+    int logit_stride;
+    SeqState* state;        // [batch]
+    uint8_t* seen;          // [batch][8194] repetition-penalty set
+    uint32_t* codes;        // [batch][code_stride]
+    int code_stride;
+    double* probs;          // [batch][8194] scratch
+    uint64_t* sortbuf;      // [batch][16384] scratch (large survivor sets)
+    float* out_scores;      // kModeProcessors output [batch][8194]
+    uint32_t* out_tokens;   // kModeDraw output
+    int draws;
+    int mode;
+    uint32_t* status;       // [batch] 0 ok, else error code (see sampler.hip)
+};
+hipError_t launch_sampler(const SampleArgs& a, int batch, hipStream_t s);
+
 // ------------------------------------------------------------------ persistent decode step
 // One launch per token for a single sequence (step.hip): grid = one 512-thread
 // workgroup per CU, all resident together; workgroups hand vectors over through the exchange buffer
 // (tagged 64-bit slots, kStepExchangeTotal of them, zero-initialised once).
 constexpr int kStepThreads = 512;
-constexpr int kStepExchange = kWidth + kQkv + kWidth + kWidth + kFfn + kHeads * kAttnMaxSplits * 68;
+// (the last kMelVocab slots: the logits, read by the fused sampling tail)
+constexpr int kStepExchange = kWidth + kQkv + kWidth + kWidth + kFfn + kHeads * kAttnMaxSplits * 68 + kMelVocab;
 // The vectors every workgroup reads (h, q|k|v, attention output, hmid, FFN activations:
 // the first kStepBroadcast slots) are also written to kStepCopies - 1 further copies
 // after the kStepExchange slots, kStepCopyStride apart, and workgroup b reads copy b % 4:
@@ -101,6 +125,7 @@ constexpr int kStepBroadcast = kWidth + kQkv + kWidth + kWidth + kFfn;
 constexpr int kStepCopies = 4;
 constexpr int kStepCopyStride = kStepBroadcast + 256;
 constexpr size_t kStepExchangeTotal = size_t(kStepExchange) + size_t(kStepCopies - 1) * kStepCopyStride;
+
 struct StepArgs {
     const void* w;            // weight slab, fp32 or bf16
     size_t layer_stride;      // elements per layer block (c_attn, c_proj, c_fc, mlp.c_proj)
@@ -126,6 +151,11 @@ struct StepArgs {
     size_t kv_slot_stride;
     int logit_stride;
     const uint8_t* table;     // beam row-owner table [nseq][kv_cap] (slot holding each row) or null
+    // fused sampling tail (step.hip decode steps; null otherwise): after its mel_head rows each
+    // workgroup counts itself in *tail; the last one samples the next token with `sample`
+    // (kModeDecode, sequence 0) in place of a separate sampler launch, and resets *tail to 0
+    uint32_t* tail;
+    SampleArgs sample;
     // measurement only (step.hip; null otherwise): workgroup b's clock at the phase ends of
     // layer l, stamps[(b * (layers + 1) + l) * 8 + k], k = 0 layer start, 1 c_attn, 2 attention
     // tiles, 3 merge, 4 attn.c_proj, 5 mlp.c_fc, 6 mlp.c_proj (l = layers: 0 head start, 6 head end)
@@ -141,28 +171,6 @@ bool step_batch_fits(int grid, int nseq);
 hipError_t step_batch_occupancy(int nseq, int* blocks_per_cu);
 hipError_t launch_step_batch(const StepArgs& a, int nseq, int grid, hipStream_t s);
 
-// ------------------------------------------------------------------ sampler
-enum SampleMode : int {
-    kModeDecode = 0,      // processors from state options + seen mask, choose, advance state
-    kModeProcessors = 1,  // processors only, write processed scores to out_scores
-    kModeDraw = 2,        // logits are already processed: draw `draws` tokens with state.rng
-};
-struct SampleArgs {
-    const float* logits;    // [batch][logit_stride]
-    int logit_stride;
-    SeqState* state;        // [batch]
-    uint8_t* seen;          // [batch][8194] repetition-penalty set
-    uint32_t* codes;        // [batch][code_stride]
-    int code_stride;
-    double* probs;          // [batch][8194] scratch
-    uint64_t* sortbuf;      // [batch][16384] scratch (large survivor sets)
-    float* out_scores;      // kModeProcessors output [batch][8194]
-    uint32_t* out_tokens;   // kModeDraw output
-    int draws;
-    int mode;
-    uint32_t* status;       // [batch] 0 ok, else error code (see sampler.hip)
-};
-hipError_t launch_sampler(const SampleArgs& a, int batch, hipStream_t s);
 
 // ------------------------------------------------------------------ beam search
 constexpr int kMaxBeamTake = 2 * kMaxBatch;

@@ -255,6 +255,12 @@ struct Engine {
     size_t per_layer = 0;       // weight elements per layer block
     DevBuf<uint64_t> xch;       // tagged exchange slots
     DevBuf<uint32_t> step_err;  // hand-off timeout flag
+    // ITTS_GPT_FUSED_SAMPLER=1: batch-1 decode steps sample the next token in the step
+    // kernel's fused tail (one launch per token).  Off by default: the tail runs the sampler on
+    // the step kernel's 512 threads, and a separate 1024-thread sampler launch measured faster
+    // (1526 against 1509 tokens/s on the 600-code workload), the same codes either way.
+    bool fused_sampling = false;
+    DevBuf<uint32_t> step_tail;  // workgroups past their mel_head rows in the running step (0 between)
     uint32_t epoch = 8;         // tag base of the next launch
     std::map<std::tuple<int, int, bool, bool>, hipGraphExec_t> graphs;
     hipEvent_t ev[4] = {};
@@ -475,6 +481,10 @@ struct Engine {
         HIP_CHECK(hipMemsetAsync(xch.p, 0, xch.n * sizeof(uint64_t), stream));
         step_err.alloc(1);
         HIP_CHECK(hipMemsetAsync(step_err.p, 0, sizeof(uint32_t), stream));
+        step_tail.alloc(1);
+        HIP_CHECK(hipMemsetAsync(step_tail.p, 0, sizeof(uint32_t), stream));
+        const char* fs = std::getenv("ITTS_GPT_FUSED_SAMPLER");
+        fused_sampling = fs && std::strcmp(fs, "1") == 0;
         step_grid = cus;
         register_step_user(dev);
         step_ok = true;
@@ -535,9 +545,14 @@ struct Engine {
         if (use_table) return nseq >= 2 && step_batch_ok[nseq] && beam_slots <= static_cast<uint32_t>(kStepBatchMax);
         return nseq == 1 || step_batch_ok[nseq];
     }
-    void launch_persistent(int nseq, bool use_table) {
+    // fuse_sampler: the single-sequence step kernel also samples the next token (its tail).
+    void launch_persistent(int nseq, bool use_table, bool fuse_sampler = false) {
         StepArgs s = step_args(0, nseq);
         s.table = use_table ? table.p : nullptr;
+        if (fuse_sampler) {
+            s.tail = step_tail.p;
+            s.sample = sample_base(kModeDecode);
+        }
         HIP_CHECK(launch_step_serialized(s, nseq, step_grid, bf16, step_dev, stream));
     }
 
@@ -659,8 +674,9 @@ struct Engine {
     void run_step(int nseq, int nb, bool sampler, bool use_table) {
         if (persistent(nseq, use_table)) {
             timing.decode_path = ITTS_PATH_STEP;
-            launch_persistent(nseq, use_table);
-            if (sampler) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
+            const bool fuse = sampler && nseq == 1 && fused_sampling;
+            launch_persistent(nseq, use_table, fuse);
+            if (sampler && !fuse) HIP_CHECK(launch_sampler(sample_base(kModeDecode), nseq, stream));
             return;
         }
         timing.decode_path = ITTS_PATH_MULTI;

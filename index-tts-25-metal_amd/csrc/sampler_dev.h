@@ -40,24 +40,31 @@ enum Status : uint32_t {
     kInvalidCode = 4,  // "GPT generated invalid semantic code"
 };
 
-struct Smem {
+// LDS of one workgroup of NTT threads working on one score row.  The decode sampler and the
+// beam kernels run 1024 threads (Smem); the persistent step kernel's fused sampling tail runs
+// its 512.  Every function below taking an SmemT works for either: only order-free parallel
+// work depends on the thread count.
+template <int NTT>
+struct SmemT {
+    static constexpr int kWaves = NTT / 64, kIpt = (V + NTT - 1) / NTT;
     union {
         float s[V];
         uint64_t sortbuf[kSortMax];
     };
     uint16_t list[V];  // finite survivors in index order; bit 15 = removed by top-p
-    uint32_t qoff[IPT][NWAVE];  // compaction: survivors before (q, wave) in index order
+    uint32_t qoff[kIpt][kWaves];  // compaction: survivors before (q, wave) in index order
     double probs[kSmallProbs];
     uint32_t hist[256];
-    uint32_t wtot[NWAVE];
-    float wmax[NWAVE];
-    uint32_t widx[NWAVE];
+    uint32_t wtot[kWaves];
+    float wmax[kWaves];
+    uint32_t widx[kWaves];
     uint32_t sel[2];
     uint32_t m;
     uint32_t token;
     uint32_t status;
     float mx;
 };
+using Smem = SmemT<NT>;
 
 __device__ __forceinline__ uint64_t splitmix_next(uint64_t& state) {
     uint64_t z = (state += 0x9E3779B97F4A7C15ull);
@@ -83,7 +90,9 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
     return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
 }
 // kk-th largest value (1-based) of s[0..V): MSB-first radix select on order-preserving keys.
-__device__ inline float radix_kth_largest(Smem& sm, uint32_t kk) {
+template <int NTT>
+__device__ inline float radix_kth_largest(SmemT<NTT>& sm, uint32_t kk) {
+    [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x, lane = t & 63;
     uint32_t prefix = 0, mask = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -137,7 +146,9 @@ __device__ inline float radix_kth_largest(Smem& sm, uint32_t kk) {
 // Compact finite entries of s into sm.list (index order); returns the count, sets sm.m and
 // sm.mx.  Entry i = t + q * NT sits at position (q, t) in index order, so a ballot per
 // (q, wave) plus one exclusive scan over the IPT x NWAVE counts places every survivor.
-__device__ inline uint32_t compact_finite(Smem& sm) {
+template <int NTT>
+__device__ inline uint32_t compact_finite(SmemT<NTT>& sm) {
+    [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     uint64_t bal[IPT];
     float mloc = -INFINITY;
@@ -193,7 +204,9 @@ __device__ inline uint32_t compact_finite(Smem& sm) {
 }
 
 // First index of the maximum (std::max_element semantics).
-__device__ inline uint32_t block_argmax(Smem& sm) {
+template <int NTT>
+__device__ inline uint32_t block_argmax(SmemT<NTT>& sm) {
+    [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     float best = -INFINITY;
     uint32_t bi = V;
@@ -230,7 +243,9 @@ __device__ inline uint32_t block_argmax(Smem& sm) {
 }
 
 // Ascending bitonic sort of sm.sortbuf[0..n), n a power of two.
-__device__ inline void bitonic_sort(Smem& sm, int n) {
+template <int NTT>
+__device__ inline void bitonic_sort(SmemT<NTT>& sm, int n) {
+    [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x;
     if (n <= 64) {
         if (t < 64) {
@@ -270,8 +285,10 @@ __device__ inline void bitonic_sort(Smem& sm, int n) {
 //   case sm.s is clobbered and the survivors are described by sm.list (index order,
 //   kRemoved flags), sm.m, sm.mx and P[0..m) (exp(double(s - mx)) of each survivor).
 // *topp_ran tells which.  Returns a Status.
-__device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ seen, float pen, float T, uint32_t top_k,
+template <int NTT>
+__device__ inline uint32_t run_processors(SmemT<NTT>& sm, const uint8_t* __restrict__ seen, float pen, float T, uint32_t top_k,
                                           float top_p, uint32_t beams, double* P_global, bool rebuild, bool* topp_ran) {
+    [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x;
     *topp_ran = false;
     if (pen != 1.0f || T != 1.0f) {
@@ -397,7 +414,8 @@ __device__ inline uint32_t run_processors(Smem& sm, const uint8_t* __restrict__ 
 // index order, target = u * total, then the first survivor whose cumulative mass exceeds
 // the target, else the last one with positive mass.  Both sums run lane-serially in index
 // order.  Returns the token, or 0xffffffff with *status set when the mass is zero.
-__device__ inline uint32_t draw_token_wave(const Smem& sm, uint32_t m, const double* P, uint64_t& rng, uint32_t* status) {
+template <int NTT>
+__device__ inline uint32_t draw_token_wave(const SmemT<NTT>& sm, uint32_t m, const double* P, uint64_t& rng, uint32_t* status) {
     const int lane = threadIdx.x & 63;
     double total = 0.0;
     for (uint32_t c0 = 0; c0 < m; c0 += 64) {
@@ -431,6 +449,119 @@ __device__ inline uint32_t draw_token_wave(const Smem& sm, uint32_t m, const dou
         }
     }
     return last_finite;
+}
+
+// One sequence's sampler pass (the body of sampler_kernel, and the fused tail of the persistent
+// step kernel): the processors and the draw on row b of the logits, then, in decode mode, the
+// token accepted and the state advanced (gpt_sampling.cpp:168-189 per step).  Every thread of
+// the workgroup calls it.
+template <int NTT>
+__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b);
+
+template <int NTT>
+__device__ inline void sample_sequence(SmemT<NTT>& sm, const SampleArgs& a, int b) {
+    [[maybe_unused]] constexpr int NT = NTT, IPT = (V + NTT - 1) / NTT;
+    const int t = threadIdx.x;
+    const SeqState& st = a.state[b];
+    if (a.mode == kModeDecode && !st.active) return;
+    const float* lg = a.logits + static_cast<size_t>(b) * a.logit_stride;
+    float v[IPT];  // all loads in flight before the first store
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+        const int i = t + q * NT;
+        v[q] = i < V ? lg[i] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+        const int i = t + q * NT;
+        if (i < V) sm.s[i] = v[q];
+    }
+    __syncthreads();
+    sample_loaded(sm, a, b);
+}
+
+// sample_sequence after the scores are in sm.s (every thread calls it; decode mode expects an
+// active state).
+template <int NTT>
+__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b) {
+    [[maybe_unused]] constexpr int NT = NTT, IPT = (V + NTT - 1) / NTT;
+    const int t = threadIdx.x;
+    SeqState& st = a.state[b];
+    const bool processors = a.mode != kModeDraw;
+    const bool need_sample = a.mode == kModeDraw || (a.mode == kModeDecode && st.do_sample);
+    if (processors && st.suppress_stop) {  // raw logits 8192 and 8193 dropped before any processor
+        if (t == 0) {
+            sm.s[kMelStart] = -INFINITY;
+            sm.s[kMelStop] = -INFINITY;
+        }
+        __syncthreads();
+    }
+    double* Pg = a.probs + static_cast<size_t>(b) * V;
+    uint32_t status = kOk;
+    bool topp = false;
+    if (processors)
+        status = run_processors(sm, a.seen + static_cast<size_t>(b) * V, st.penalty, st.temperature, st.top_k, st.top_p,
+                                st.num_beams, Pg, a.mode == kModeProcessors, &topp);
+    uint32_t token = 0;
+    if (status == kOk) {
+        if (a.mode == kModeProcessors) {
+            float* out = a.out_scores + static_cast<size_t>(b) * V;
+            for (int i = t; i < V; i += NT) out[i] = sm.s[i];
+        } else if (!need_sample) {
+            token = block_argmax(sm);  // greedy: std::max_element
+        } else {
+            uint32_t m = sm.m;
+            if (!topp) {
+                m = compact_finite(sm);
+                if (m == 0) status = kNoFinite;
+                else {
+                    double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : Pg;
+                    const float mx = sm.mx;
+                    for (uint32_t j = t; j < m; j += NT) P[j] = libm::exp_glibc(static_cast<double>(sm.s[sm.list[j]] - mx));
+                    __syncthreads();
+                }
+            }
+            if (status == kOk && t < 64) {
+                // wave 0 draws; every lane holds the same rng, token and status
+                const double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : Pg;
+                uint64_t rng = st.rng;
+                const int draws = a.mode == kModeDraw ? a.draws : 1;
+                for (int d = 0; d < draws && status == kOk; ++d) {
+                    token = draw_token_wave(sm, m, P, rng, &status);
+                    if (a.mode == kModeDraw && t == 0) a.out_tokens[d] = token;
+                }
+                if (t == 0) st.rng = rng;
+            }
+        }
+    }
+    if (t != 0) return;
+    a.status[b] = status;
+    if (a.mode != kModeDecode) return;
+    if (status != kOk) {
+        st.error = 1;
+        st.active = 0;
+        return;
+    }
+    // Accept the token and advance the state (gpt_sampling.cpp:181-186).
+    if (token == static_cast<uint32_t>(kMelStop)) {
+        st.stopped = 1;
+        st.active = 0;
+    } else if (token >= static_cast<uint32_t>(kMelStart)) {
+        a.status[b] = kInvalidCode;
+        st.error = 1;
+        st.active = 0;
+    } else {
+        a.codes[static_cast<size_t>(b) * a.code_stride + st.count] = token;
+        st.count += 1;
+        a.seen[static_cast<size_t>(b) * V + token] = 1;
+        if (st.count >= st.max_tokens) {
+            st.active = 0;
+        } else {
+            st.token = token;
+            st.position = st.count + 1;  // the first generated code sits at mel position 2
+            st.n = st.prefix_rows + st.count - 1;
+        }
+    }
 }
 
 }  // namespace sampling

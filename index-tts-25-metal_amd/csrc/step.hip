@@ -48,6 +48,7 @@
 // mit2_linear_gemv_f32 (1054-1080), mit2_layernorm_f32_rows (618-669),
 // mit2_gpt_cached_attention_resident_f32 (2064-2145), mit2_gelu_f32 (486-503),
 // mit2_add_f32 (161-171), mit2_gpt_build_current_f32 (1310-1324).
+#include "sampler_dev.h"
 #include "step_common.h"
 
 namespace itts {
@@ -358,10 +359,76 @@ constexpr int kGQkv = 1, kGProj = 1, kGFc = 2, kGFc2 = 1, kGHead = 3;
 // Attention merges of at most this many splits run from registers (KV up to 1024 rows).
 constexpr int kMergeRegSplits = 16;
 
+// The workgroup's LDS: the weight ring and the phase buffers while the step runs; the
+// sampler's buffers in the fused sampling tail, after every wave is done with the former.
+struct StepLds {
+    float ring[kRing * kChunkF];
+    Smem sm;
+};
+union StepTailLds {
+    StepLds step;
+    sampling::SmemT<kST> samp;
+};
+
+// The fused sampling tail (gpt_sampling.cpp:168-189 for the step's token), run by all eight
+// waves of every workgroup after their last step work.  Each workgroup has stored its
+// mel_head rows also as tagged exchange slots {logit, epoch}; it counts itself in, and the
+// last to arrive (nobody waits for a count) reads the whole row from those slots (re-reading
+// any slot whose tag is not yet this launch's, with the bounded wait of every hand-off) and
+// samples from it exactly as sampler_kernel does, with its 512 threads, then resets the
+// counter for the next launch.  The tags make the data's arrival explicit, so no device-wide
+// fence (an L2 write-back) is needed.  This replaces a separate sampler launch per token.
+__device__ inline void sampling_tail(const StepArgs& a, Ctl& ctl, StepTailLds& lds, uint32_t e) {
+    if (!a.tail) return;
+    __syncthreads();  // the second full barrier of the kernel: loaders and compute waves all here
+    const int tid = threadIdx.x;
+    if (tid == 0)
+        ctl.last = __hip_atomic_fetch_add(a.tail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!ctl.last) return;
+    if (tid == 0) __hip_atomic_store(a.tail, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!a.state->active) return;
+    auto& sm = lds.samp;
+    constexpr int kPer = (kMelVocab + kST - 1) / kST;
+    uint64_t v[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int i = tid + q * kST;
+        v[q] = i < kMelVocab ? xld(a.xch + kXlogit + i) : (static_cast<uint64_t>(e) << 32);
+    }
+    bool failed = false;
+    for (unsigned spins = 0;;) {
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) ok &= static_cast<uint32_t>(v[q] >> 32) == e;
+        if (ok) break;
+        if (++spins > kSpinLimit) {
+            atomicOr(a.err, 1u);
+            failed = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = tid + q * kST;
+            if (static_cast<uint32_t>(v[q] >> 32) != e) v[q] = xld(a.xch + kXlogit + i);
+        }
+    }
+    (void)failed;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int i = tid + q * kST;
+        if (i < kMelVocab) sm.s[i] = __uint_as_float(static_cast<uint32_t>(v[q]));
+    }
+    __syncthreads();
+    sampling::sample_loaded(sm, a.sample, 0);
+}
+
 __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
-    __shared__ float ring[kRing * kChunkF];
+    __shared__ StepTailLds lds;
     __shared__ Ctl ctl;
-    __shared__ Smem sm;
+    float* ring = lds.step.ring;
+    Smem& sm = lds.step.sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const SeqState st = *a.state;
     if (!st.active) return;
@@ -384,6 +451,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
     if (wave >= kCW) {
         wait_go(ctl, a.err);
         run_loader(a, P, ring, ctl, __builtin_amdgcn_readfirstlane(wave - kCW), lane);
+        sampling_tail(a, ctl, lds, a.epoch + 8u * static_cast<uint32_t>(a.layers) + kEpLogit);
         return;
     }
 
@@ -844,11 +912,15 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             ln_stats(v, mean, inv);
             ln_to_xrow(sm.xs, lane, mean, inv, fn, x);
         }
-        auto out = [&](int k, float b, float acc) { a.logits[P.h0 + k] = acc + b; };
+        auto out = [&](int k, float b, float acc) {
+            a.logits[P.h0 + k] = acc + b;
+            if (a.tail) xst(X + kXlogit + P.h0 + k, ep(a.layers, kEpLogit), acc + b);
+        };
         gemv_rows(ctl, ring, chd, P.hn, x, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
         release_to(ctl, total_chunks, wave);
     }
     stamp(a.layers, 6);
+    sampling_tail(a, ctl, lds, ep(a.layers, kEpLogit));
 }
 
 }  // namespace

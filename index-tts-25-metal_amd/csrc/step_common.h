@@ -36,10 +36,11 @@ constexpr int kXattn = kXqkv + kQkv;
 constexpr int kXhmid = kXattn + kWidth;
 constexpr int kXff = kXhmid + kWidth;
 constexpr int kXpart = kXff + kFfn;
-static_assert(kXpart + kHeads * kAttnMaxSplits * 68 == kStepExchange, "exchange layout");
+constexpr int kXlogit = kXpart + kHeads * kAttnMaxSplits * 68;
+static_assert(kXlogit + kMelVocab == kStepExchange, "exchange layout");
 static_assert(kXpart == kStepBroadcast, "broadcast vectors come first");
 
-enum Kind : uint32_t { kEpXh = 0, kEpQkv = 1, kEpPart = 2, kEpAttn = 3, kEpHmid = 4, kEpFf = 5 };
+enum Kind : uint32_t { kEpXh = 0, kEpQkv = 1, kEpPart = 2, kEpAttn = 3, kEpHmid = 4, kEpFf = 5, kEpLogit = 6 };
 
 __device__ __forceinline__ uint64_t xld(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 // base + 32-bit unsigned element offset (a scalar base plus one VGPR per address)
@@ -137,6 +138,7 @@ struct alignas(16) Ctl {
     uint32_t need[kCW];  // compute wave c: first chunk it may still read
     uint32_t bar;        // compute-wave barrier arrivals
     uint32_t go;         // step.hip: set once layer 0's input row has arrived; loaders start then
+    uint32_t last;       // step.hip: this workgroup was the last to finish its mel_head rows
 };
 
 // A loader wave's wait for ctl.go (bounded like every wait of the step kernels).

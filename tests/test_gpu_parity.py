@@ -418,6 +418,36 @@ def test_persistent_generate_equals_multikernel(both_paths, itts):
     assert step.cached_tokens() == multi.cached_tokens()
 
 
+def test_fused_sampling_tail_equals_separate_sampler(itts, small_weights):
+    """ITTS_GPT_FUSED_SAMPLER=1: the step kernel's last workgroup samples the next token from the
+    tagged logits (512 threads) instead of a sampler launch (1024 threads): same codes, sampled
+    (top-k/top-p, penalty, temperature), greedy, and with a stop token allowed."""
+    import os
+
+    old = os.environ.get("ITTS_GPT_FUSED_SAMPLER")
+    try:
+        os.environ["ITTS_GPT_FUSED_SAMPLER"] = "1"
+        fused = itts.GptDecoder(small_weights, kv_capacity=1024)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_FUSED_SAMPLER"]
+        else:
+            os.environ["ITTS_GPT_FUSED_SAMPLER"] = old
+    plain = itts.GptDecoder(small_weights, kv_capacity=1024)
+    cond, text = itts.synthetic_prefix_inputs(60, seed=7)
+    prefix = fused.prepare_cond(cond, text, 0)
+    for o in (itts.GenerationOptions(do_sample=True, seed=11, suppress_stop=True),
+              itts.GenerationOptions(do_sample=True, seed=12, top_k=0, top_p=0.9, temperature=1.1, repetition_penalty=2.0),
+              itts.GenerationOptions(do_sample=False, repetition_penalty=1.0, suppress_stop=True)):
+        a = fused.generate(prefix, o, 80)
+        assert fused.last_timing()["decode_path"] == "step"
+        b = plain.generate(prefix, o, 80)
+        assert (a.codes, a.stopped) == (b.codes, b.stopped), o
+        assert fused.cached_tokens() == plain.cached_tokens()
+    fused.close()
+    plain.close()
+
+
 def test_two_decoders_concurrently_on_one_gpu(itts, small_weights):
     """Two decoders of one process on one GPU, each driven from its own thread, both on the
     persistent step (batch 1 and batch 2): their grids are chained, never resident together,

@@ -231,17 +231,23 @@ struct GemmArgs {
     uint32_t kv_cap;
     const uint32_t* row_slot;
     const uint32_t* row_pos;
-    // split-K: K is cut into `splits` equal ranges (a multiple of 16 each); the partial
-    // tiles go to ws[splits][M][N] and a second kernel adds them in split order
+    // split-K: at most `splits` K ranges (multiples of 128); launch_gemm picks the row
+    // blocking and the split count from an estimate of the time.  The partial tiles go to
+    // ws[splits][M][N] and a second kernel adds them in split order.
     int splits;             // 1: no split
     float* ws;
+    // kGemmResid with ln_out (N = 1280): also ln_out[m] = LayerNorm(c[m]; ln_w, ln_b), the
+    // next LayerNorm of the residual stream (kernels.metal:618-669), folded into the split-K
+    // reduce when there is one
+    const float* ln_w;
+    const float* ln_b;
+    float* ln_out;
 };
-// Split-K is used while the output tiles number fewer than kGemmTargetTiles / 2: up to
-// kGemmMaxSplits splits, as many as keep tiles * splits <= kGemmTargetTiles.  The
-// workspace then holds splits * M * N <= kGemmTargetTiles * 64 * 64 floats.
-constexpr int kGemmTargetTiles = 512;
-constexpr int kGemmMaxSplits = 8;
-constexpr size_t kGemmWsFloats = size_t(kGemmTargetTiles) * 64 * 64;
+// The workspace holds kGemmWsFloats floats, which bounds splits * M * N.
+constexpr int kGemmMaxSplits = 16;
+constexpr size_t kGemmWsFloats = size_t(512) * 64 * 64;
+// The split count launch_gemm would use for this shape (callers pass it in GemmArgs.splits;
+// 1 forbids splitting).
 int gemm_splits(int M, int N, int K);
 hipError_t launch_gemm(const GemmArgs& a, int epi, bool bf16, hipStream_t s);
 

@@ -757,7 +757,8 @@ struct Engine {
         float *px_ = b.x, *pxn_ = b.xn, *pq_ = b.q, *patt_ = b.att, *pff_ = b.ff;
         for (int l = 0; l < layers; ++l) {
             const float* par = params.p + static_cast<size_t>(l) * kParLayer;
-            HIP_CHECK(launch_ln_rows(LnRowsArgs{px_, pxn_, par + kParLn1W, par + kParLn1B, static_cast<int>(M)}, stream));
+            // layers after the first get ln_1 from the previous layer's mlp.c_proj launch
+            if (l == 0) HIP_CHECK(launch_ln_rows(LnRowsArgs{px_, pxn_, par + kParLn1W, par + kParLn1B, static_cast<int>(M)}, stream));
             GemmArgs g{};
             g.a = pxn_;
             g.w = w_ptr(off_qkv[l]);
@@ -798,8 +799,10 @@ struct Engine {
             p.splits = gemm_splits(static_cast<int>(M), kWidth, kWidth);
             p.ws = b.ws;
             p.c = px_;
+            p.ln_w = par + kParLn2W;  // ln_2 of the new residual rows
+            p.ln_b = par + kParLn2B;
+            p.ln_out = pxn_;
             HIP_CHECK(launch_gemm(p, kGemmResid, bf16, stream));
-            HIP_CHECK(launch_ln_rows(LnRowsArgs{px_, pxn_, par + kParLn2W, par + kParLn2B, static_cast<int>(M)}, stream));
             GemmArgs f{};
             f.a = pxn_;
             f.w = w_ptr(off_fc[l]);
@@ -821,6 +824,11 @@ struct Engine {
             f2.splits = gemm_splits(static_cast<int>(M), kWidth, kFfn);
             f2.ws = b.ws;
             f2.c = px_;
+            if (l + 1 < layers) {  // ln_1 of the next layer
+                f2.ln_w = par + kParLayer + kParLn1W;
+                f2.ln_b = par + kParLayer + kParLn1B;
+                f2.ln_out = pxn_;
+            }
             HIP_CHECK(launch_gemm(f2, kGemmResid, bf16, stream));
         }
         HIP_CHECK(launch_gather_rows(px_, b.last_rows, h.p, nseq, stream));

@@ -108,6 +108,21 @@ def test_prefill_and_steps_small(small):
     assert dec.cached_tokens() == orc.cached_tokens()
 
 
+@pytest.mark.parametrize("n_text", [1, 13, 29, 61, 93, 125, 157, 253, 480])
+def test_prefill_row_counts_match_oracle(small, itts, n_text):
+    """Prefill logits and the next step against the oracle for prefixes of 36..515 rows: the
+    prefill GEMM picks its row blocking (16..192 rows per block) and K split from the row
+    count, the last row block holds clamped rows past the prefix, and the causal attention
+    walks one to nine 64-key chunks.  The step after it reads the K/V rows the prefill wrote."""
+    dec, orc, cond, _ = small
+    _, text = itts.synthetic_prefix_inputs(n_text, seed=100 + n_text)
+    prefix = dec.prepare_cond(cond, text, 0)
+    rows = prefix.size // 1280
+    print(f"prefill rows {rows}", flush=True)
+    assert_logits_close(dec.prefill(prefix), orc.prefill(prefix), f"prefill {rows} rows")
+    assert_logits_close(dec.step(17, 2), orc.step(17, 2), f"step after {rows} rows")
+
+
 def test_step_errors(small, itts):
     dec, orc, cond, text = small
     dec.prefill(dec.prepare_cond(cond, text, 0))

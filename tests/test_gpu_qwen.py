@@ -80,6 +80,18 @@ def test_long_prompt_and_steps_across_splits(pair):
     w.report()
 
 
+def test_steps_past_1024_rows(pair):
+    """A 1010-id prompt (16 attention splits) and 30 steps: the cache crosses row 1024, and the
+    split merge runs over 16 and then 17 splits."""
+    dec, orc = pair
+    w = Worst("qwen 2-layer, 1010-id prompt + 30 steps")
+    p = ids_of(5, 1040)
+    w.check(dec.prefill(p[:1010]), orc.prefill(p[:1010]), "prefill")
+    for i in range(1010, 1040):
+        w.check(dec.step(p[i]), orc.step(p[i]), f"step at row {i}")
+    w.report()
+
+
 def test_greedy_generate_matches_oracle(pair):
     dec, orc = pair
     for n, maximum in ((12, 40), (130, 16), (5, 1)):

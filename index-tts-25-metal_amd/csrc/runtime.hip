@@ -1250,13 +1250,15 @@ struct Engine {
 
     // Device-to-device copy of 256 MiB of the weight slab (a plain copy kernel of known
     // size, the reference point for HBM traffic counters): bytes = read + written.
-    // Phases of the persistent batch-1 step at `cached_rows` cached rows, from the kernel's own
-    // clock stamps (100 MHz): T_k(l) = the latest workgroup's end of phase k of layer l; the
-    // phase's share of the step is T_k - T_{k-1} (T_0 = the latest layer start).  out[0] mean
-    // layer time, out[1..6] mean phase shares (c_attn, attention tiles, merge, attn.c_proj,
-    // mlp.c_fc, mlp.c_proj), out[7] the head (ln_f, final_norm, mel_head), all in us.
-    void step_phases(uint32_t cached_rows, int iters, float* out) {
-        if (!layers || iters < 1 || !persistent(1, false)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
+    // Phases of the persistent step (batch 1) or batch step (nseq 2-4 sequences, each at
+    // `cached_rows` cached rows) from the kernel's own clock stamps (100 MHz): T_k(l) = the
+    // latest workgroup's end of phase k of layer l; the phase's share of the step is
+    // T_k - T_{k-1} (T_0 = the latest layer start).  out[0] mean layer time, out[1..6] mean
+    // phase shares (c_attn, attention tiles, merge, attn.c_proj, mlp.c_fc, mlp.c_proj), out[7]
+    // the head (ln_f, final_norm, mel_head), all in us.
+    void step_phases(uint32_t cached_rows, int iters, float* out, int nseq = 1) {
+        if (!layers || iters < 1 || nseq < 1 || nseq > static_cast<int>(max_batch) || !persistent(nseq, false))
+            throw std::invalid_argument("The persistent step kernel is not available on this decoder");
         if (!cached_rows) cached_rows = 752;
         if (cached_rows + 1 >= cap) throw std::invalid_argument("Invalid kernel benchmark request");
         itts_gen_options o;
@@ -1264,8 +1266,8 @@ struct Engine {
         SeqState st = make_state(o, cached_rows, 2);
         st.token = 1;
         st.position = 2;
-        pinned_state[0] = st;
-        upload_states(1);
+        for (int q = 0; q < nseq; ++q) pinned_state[q] = st;
+        upload_states(nseq);
         const size_t per = static_cast<size_t>(layers + 1) * kStepStampsPerLayer;
         DevBuf<uint64_t> stamps;
         stamps.alloc(static_cast<size_t>(step_grid) * per);
@@ -1273,9 +1275,9 @@ struct Engine {
         std::vector<double> sum(8, 0.0);
         for (int it = 0; it <= iters; ++it) {  // launch 0 warms up
             HIP_CHECK(hipMemsetAsync(stamps.p, 0, stamps.n * 8, stream));
-            StepArgs a = step_args(0, 1);
+            StepArgs a = step_args(0, nseq);
             a.stamps = stamps.p;
-            HIP_CHECK(launch_step_serialized(a, 1, step_grid, bf16, step_dev, stream));
+            HIP_CHECK(launch_step_serialized(a, nseq, step_grid, bf16, step_dev, stream));
             HIP_CHECK(hipMemcpyAsync(host.data(), stamps.p, stamps.n * 8, hipMemcpyDeviceToHost, stream));
             HIP_CHECK(hipStreamSynchronize(stream));
             check_step_error();
@@ -1804,6 +1806,13 @@ int itts_gpt_step_phases(itts_gpt* h, uint32_t cached_rows, uint32_t iters, floa
     return guarded(h, [&] {
         if (!phase_us) throw std::invalid_argument("Invalid kernel benchmark request");
         h->e.step_phases(cached_rows, static_cast<int>(iters), phase_us);
+    });
+}
+
+int itts_gpt_step_phases_batch(itts_gpt* h, uint32_t nseq, uint32_t cached_rows, uint32_t iters, float* phase_us) {
+    return guarded(h, [&] {
+        if (!phase_us || nseq < 2 || nseq > static_cast<uint32_t>(itts::kStepBatchMax)) throw std::invalid_argument("Invalid kernel benchmark request");
+        h->e.step_phases(cached_rows, static_cast<int>(iters), phase_us, static_cast<int>(nseq));
     });
 }
 

@@ -139,6 +139,7 @@ struct SmemB {
     float resid_h[B][kResidMax];  // h at this workgroup's attn.c_proj rows (their residual)
     float resid_m[B][kResidMax];  // hmid at this workgroup's mlp.c_proj rows
     float redm[4], reds[4];
+    float lnst[B][2];  // LayerNorm mean and 1 / sqrt(var + eps) of each sequence's row
     float accs[16][kHeadDim + 4];
 };
 
@@ -200,25 +201,34 @@ __device__ __forceinline__ void load_rows(const float* base, const uint32_t (&of
 constexpr int kQWin = 4;    // rounds whose q / new K / new V are polled together
 constexpr int kQRec = 192;  // floats per round in the window: q, new K, new V (64 each)
 
-// dst[q] = LayerNorm(row[q]) for this thread's 5 columns (tid + 256 i) of each of B rows; the
-// statistics are those of ln_stats (every wave forms them for the whole row), so the values
-// equal ln_to_xrow's.  All rows are read before any is written, so the B reductions run
-// interleaved (row by row, each output store would have to precede the next row's loads).
+// stage[q][dst + c] = LayerNorm(stage[q][src + c]) for this thread's 5 columns c = tid + 256 i
+// of each of the B staging rows.  Compute wave q (< B) forms row q's statistics with ln_stats
+// (so the values equal ln_to_xrow's) and passes them through lnst across one compute-wave
+// barrier; every thread then normalises its own columns.  (Each wave forming every row's
+// statistics itself, as the batch-1 kernel does to save the barrier, costs B times the LDS
+// reads and reductions.)
 template <int B>
-__device__ __forceinline__ void ln_rows_to(const float* const (&row)[B], float* const (&dst)[B], const LnPar& p, int tid, int lane) {
-    float v[B][4][5], mean[B], inv[B], own[B][5];
+__device__ __forceinline__ void ln_stage_rows(float (*stage)[kFfn], int src, int dst, const LnPar& p, int tid, int lane,
+                                              float (*lnst)[2], Ctl& ctl, uint32_t& gen, uint32_t* err, bool& failed) {
+    static_assert(B <= kCW, "one compute wave per row's statistics");
+    const int wave = tid >> 6;
+    if (wave < B) {
+        float v[4][5], mean, inv;
+        ln_layout_load(stage[wave] + src, lane, v);
+        ln_stats(v, mean, inv);
+        if (lane == 0) {
+            lnst[wave][0] = mean;
+            lnst[wave][1] = inv;
+        }
+    }
+    cbar(ctl, gen, err, failed);
 #pragma unroll
     for (int q = 0; q < B; ++q) {
-        ln_layout_load(row[q], lane, v[q]);
+        const float mean = lnst[q][0], inv = lnst[q][1];
 #pragma unroll
-        for (int i = 0; i < 5; ++i) own[q][i] = row[q][tid + 256 * i];
+        for (int i = 0; i < 5; ++i)
+            stage[q][dst + tid + 256 * i] = ln_apply(stage[q][src + tid + 256 * i], mean, inv, p.g[i], p.b[i]);
     }
-#pragma unroll
-    for (int q = 0; q < B; ++q) ln_stats(v[q], mean[q], inv[q]);
-#pragma unroll
-    for (int q = 0; q < B; ++q)
-#pragma unroll
-        for (int i = 0; i < 5; ++i) dst[q][tid + 256 * i] = ln_apply(own[q][i], mean[q], inv[q], p.g[i], p.b[i]);
 }
 
 // rowsN of step.hip for B inputs: rows k0 + 4 t (t < N, those below cnt) of a 1280-wide slice,
@@ -391,11 +401,17 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
     auto ep = [&](int l, uint32_t kind) { return e0 + 8u * static_cast<uint32_t>(l) + kind; };
     auto XW = [&](int q) { return xregion(a.xch, q); };                                  // written by producers
     auto XR = [&](int q) -> const uint64_t* { return xregion(a.xch, q) + xcopy(cpy, 0); };  // this workgroup's copy
+    // phase-end clocks for measurement (one lane, only when the host asks for them)
+    auto stamp = [&](int l, int k) {
+        if (a.stamps && opaque_tid() == 0)
+            a.stamps[(static_cast<size_t>(P.b) * (a.layers + 1) + l) * kStepStampsPerLayer + k] = __builtin_amdgcn_s_memrealtime();
+    };
 
     for (int l = 0; l < a.layers; ++l) {
         const float* __restrict__ par = a.params + static_cast<size_t>(l) * kParLayer;
         const size_t kvl = static_cast<size_t>(l) * a.kv_layer_stride;
         const int cb = l * P.layer_chunks;
+        stamp(l, 0);
 
         // ------------------------------------------------ LN1 + c_attn (+ K/V append)
         {
@@ -436,16 +452,7 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
 #pragma unroll
                 for (int q = 0; q < B; ++q) sm.resid_h[q][lane] = sm.stage[q][P.p0 + lane];
             }
-            {
-                const float* rows[B];
-                float* dst[B];
-#pragma unroll
-                for (int q = 0; q < B; ++q) {
-                    rows[q] = sm.stage[q];
-                    dst[q] = sm.stage[q] + kWidth;
-                }
-                ln_rows_to<B>(rows, dst, ln, tid, lane);
-            }
+            ln_stage_rows<B>(sm.stage, 0, kWidth, ln, tid, lane, sm.lnst, ctl, gen, a.err, failed);
             cbar(ctl, gen, a.err, failed);
             const float* x[B];
 #pragma unroll
@@ -467,6 +474,8 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             gemv_rows_b<B, RING, C::kFive>(ctl, ring, cb, P.qn, x, bias, par + kParQkvB + P.q0, wave, lane, a.err, failed, out);
             stores_done();
         }
+
+        stamp(l, 1);
 
         // ------------------------------------------------ split-KV attention tiles
         {
@@ -588,6 +597,8 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             stores_done();
         }
 
+        stamp(l, 2);
+
         // ------------------------------------------------ merge of (sequence, head) = (b / 20, b % 20)
         if (P.b < kHeads * B) {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
@@ -675,6 +686,8 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             }
         }
 
+        stamp(l, 3);
+
         // ------------------------------------------------ attn.c_proj + residual
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
@@ -710,6 +723,8 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             cbar(ctl, gen, a.err, failed);  // the staging area is written by the next phase
         }
 
+        stamp(l, 4);
+
         // ------------------------------------------------ LN2 + c_fc + GELU
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
@@ -740,16 +755,7 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
 #pragma unroll
                 for (int q = 0; q < B; ++q) sm.resid_m[q][lane] = sm.stage[q][P.g0 + lane];
             }
-            {
-                const float* rows[B];
-                float* dst[B];
-#pragma unroll
-                for (int q = 0; q < B; ++q) {
-                    rows[q] = sm.stage[q];
-                    dst[q] = sm.stage[q] + kWidth;
-                }
-                ln_rows_to<B>(rows, dst, ln, tid, lane);
-            }
+            ln_stage_rows<B>(sm.stage, 0, kWidth, ln, tid, lane, sm.lnst, ctl, gen, a.err, failed);
             cbar(ctl, gen, a.err, failed);
             const float* x[B];
 #pragma unroll
@@ -761,6 +767,8 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             stores_done();
             cbar(ctl, gen, a.err, failed);  // the staging area is written by the next phase
         }
+
+        stamp(l, 5);
 
         // ------------------------------------------------ mlp.c_proj + residual -> next h
         {
@@ -815,7 +823,9 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             stores_done();
             cbar(ctl, gen, a.err, failed);  // the staging area is written by the next phase
         }
+        stamp(l, 6);
     }
+    stamp(a.layers, 0);
 
     // ---------------------------------------------------- ln_f, final_norm, mel_head
     {
@@ -846,27 +856,9 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
         }
         cbar(ctl, gen, a.err, failed);
         // ln_f, then final_norm, each into the next 1280 floats of the sequence's staging row
-        {
-            const float* rows[B];
-            float* dst[B];
-#pragma unroll
-            for (int q = 0; q < B; ++q) {
-                rows[q] = sm.stage[q];
-                dst[q] = sm.stage[q] + kWidth;
-            }
-            ln_rows_to<B>(rows, dst, lf, tid, lane);
-        }
+        ln_stage_rows<B>(sm.stage, 0, kWidth, lf, tid, lane, sm.lnst, ctl, gen, a.err, failed);
         cbar(ctl, gen, a.err, failed);
-        {
-            const float* rows[B];
-            float* dst[B];
-#pragma unroll
-            for (int q = 0; q < B; ++q) {
-                rows[q] = sm.stage[q] + kWidth;
-                dst[q] = sm.stage[q] + 2 * kWidth;
-            }
-            ln_rows_to<B>(rows, dst, fn, tid, lane);
-        }
+        ln_stage_rows<B>(sm.stage, kWidth, 2 * kWidth, fn, tid, lane, sm.lnst, ctl, gen, a.err, failed);
         cbar(ctl, gen, a.err, failed);
         const float* x[B];
 #pragma unroll
@@ -875,6 +867,7 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
         gemv_rows_b<B, RING, C::kFive>(ctl, ring, chd, P.hn, x, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
         release_to(ctl, total_chunks, wave);
     }
+    stamp(a.layers, 6);
 }
 
 template <int B>

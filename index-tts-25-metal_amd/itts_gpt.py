@@ -111,6 +111,7 @@ def _load() -> C.CDLL:
         "itts_gpt_last_timing": (C.c_int, [P, C.POINTER(_Timing)]),
         "itts_gpt_bench_kernel": (C.c_int, [P, i32, u32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
         "itts_gpt_step_phases": (C.c_int, [P, u32, u32, C.POINTER(C.c_float)]),
+        "itts_gpt_step_phases_batch": (C.c_int, [P, u32, u32, u32, C.POINTER(C.c_float)]),
         "itts_synthetic_normal": (None, [f32p, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
         "itts_bundle_open": (C.c_int, [C.c_char_p, i32, C.POINTER(P)]),
         "itts_bundle_close": (None, [P]),
@@ -521,10 +522,14 @@ class GptDecoder:
     # Processors / sampler on this handle's stream.
     STEP_PHASES = ("layer", "c_attn", "attention_tiles", "merge", "attn_proj", "mlp_fc", "mlp_proj", "head")
 
-    def step_phases(self, cached_rows: int = 0, iters: int = 20) -> dict:
-        """Per-phase time (us) of the persistent step kernel from its own clock stamps."""
+    def step_phases(self, cached_rows: int = 0, iters: int = 20, nseq: int = 1) -> dict:
+        """Per-phase time (us) of the persistent step kernel (nseq 1) or batch step kernel
+        (nseq 2-4 sequences, each at cached_rows) from its own clock stamps."""
         out = (C.c_float * 8)()
-        self._check(_lib.itts_gpt_step_phases(self._h, int(cached_rows), int(iters), out))
+        if nseq == 1:
+            self._check(_lib.itts_gpt_step_phases(self._h, int(cached_rows), int(iters), out))
+        else:
+            self._check(_lib.itts_gpt_step_phases_batch(self._h, int(nseq), int(cached_rows), int(iters), out))
         return {k: float(v) for k, v in zip(self.STEP_PHASES, out)}
 
     def apply_processors(self, logits: np.ndarray, history: Sequence[int], options: GenerationOptions) -> np.ndarray:

@@ -202,68 +202,140 @@ __device__ uint32_t block_scan(uint32_t c, uint32_t* wtot, uint32_t* total) {
 // Sampled candidate selection for sampled beams when at most kLdsCands scores are
 // finite, by wave 0 with the candidates in LDS: take draws without replacement, each
 // (gpt_sampling.cpp:130-165 on the remaining candidates) with its maximum, its total and
-// its cumulative scan in index order.  The weights exp(double(score - max)) are recomputed
-// per pass (the same values).  Returns kOk or the failing status; ids[0..take) on success.
+// its cumulative scan in index order.
+// - Weights: w[j] = exp(double(score_j - max)), 0 for drawn candidates, in pw.  They are
+//   recomputed only when the maximum changes (the same values otherwise); pw is padded
+//   with zeros to a multiple of 8.
+// - Total: lane 0 adds w[0], w[1], ... in index order (the reference's total) and keeps
+//   each partial sum in pre[j].  The reference's cumulative walk skips zero weights and
+//   adds the others in the same order, so its running value at candidate j is pre[j] too:
+//   the pick, the first j with w[j] > 0 and target < pre[j] (else the last j with
+//   w[j] > 0), is found with one ballot per 64 candidates instead of a second serial pass.
+// Returns kOk or the failing status; ids[0..take) on success.
 constexpr int kLdsCands = 2048;
-__device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, uint32_t F, int take, uint64_t& rng, uint32_t* ids) {
+__device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, double* pw, double* pre, uint32_t F, int take, uint64_t& rng,
+                                         uint32_t* ids) {
     const int lane = threadIdx.x & 63;
     constexpr uint32_t kTaken = 0x80000000u;
+    constexpr uint32_t kNone = 0xffffffffu;
+    const uint32_t F8 = (F + 7u) & ~7u;
+    float mprev = NAN;
     for (int d = 0; d < take; ++d) {
         float m = -INFINITY;  // max over the still-available entries
         for (uint32_t j = lane; j < F; j += 64)
             if (!(lid[j] & kTaken)) m = fmaxf(m, lsc[j]);
         m = wave_max(m);
         if (m == -INFINITY) return kNoFinite;
-        // Up to 128 candidates: each weight is evaluated once per draw (registers pa, pb) and
-        // used by both passes below; more candidates are re-evaluated in the second pass.
-        const bool small = F <= 128;
-        double pa = 0.0, pb = 0.0;
-        if (small) {
-            if (lane < F && !(lid[lane] & kTaken)) pa = libm::exp_glibc(static_cast<double>(lsc[lane] - m));
-            if (64 + lane < F && !(lid[64 + lane] & kTaken)) pb = libm::exp_glibc(static_cast<double>(lsc[64 + lane] - m));
+        if (!(m == mprev)) {
+            for (uint32_t j = lane; j < F8; j += 64)
+                pw[j] = j < F && !(lid[j] & kTaken) ? libm::exp_glibc(static_cast<double>(lsc[j] - m)) : 0.0;
+            mprev = m;
         }
-        auto weight = [&](uint32_t c0) -> double {
-            if (small) return c0 == 0 ? pa : pb;
-            const uint32_t j = c0 + lane;
-            return j < F && !(lid[j] & kTaken) ? libm::exp_glibc(static_cast<double>(lsc[j] - m)) : 0.0;
-        };
         double total = 0.0;
-        for (uint32_t c0 = 0; c0 < F; c0 += 64) {
-            const double p = weight(c0);
-            const int cn = static_cast<int>(min(64u, F - c0));
-            for (int q = 0; q < cn; ++q) total += readlane_f64(p, q);
-        }
-        if (total <= 0.0) return kZeroMass;
-        const double target = splitmix_unit(rng) * total;
-        double cumulative = 0.0;
-        uint32_t pick = 0xffffffffu, last = 0xffffffffu;
-        for (uint32_t c0 = 0; c0 < F && pick == 0xffffffffu; c0 += 64) {
-            const double p = weight(c0);
-            const int cn = static_cast<int>(min(64u, F - c0));
-            for (int q = 0; q < cn; ++q) {
-                const double pq = readlane_f64(p, q);
-                if (pq <= 0.0) continue;
-                last = c0 + static_cast<uint32_t>(q);
-                cumulative += pq;
-                if (target < cumulative) {
-                    pick = last;
-                    break;
+        if (lane == 0) {
+            // w[j] in index order; each chunk of 8 is read while the previous one is added
+            const double2* w2 = reinterpret_cast<const double2*>(pw);
+            double2* p2 = reinterpret_cast<double2*>(pre);
+            double2 c[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] = w2[k];
+            for (uint32_t j = 0; j < F8; j += 8) {
+                const uint32_t nx = min(j + 8, F8 - 8) >> 1;  // in bounds; unused past the end
+                double2 n[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) n[k] = w2[nx + k];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    double2 r;
+                    total += c[k].x;
+                    r.x = total;
+                    total += c[k].y;
+                    r.y = total;
+                    p2[(j >> 1) + k] = r;
                 }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) c[k] = n[k];
             }
         }
-        if (pick == 0xffffffffu) pick = last;
+        total = __shfl(total, 0, 64);
+        if (total <= 0.0) return kZeroMass;
+        const double target = splitmix_unit(rng) * total;
+        uint32_t pick = kNone, last = kNone;
+        for (uint32_t c0 = 0; c0 < F; c0 += 64) {
+            const uint32_t j = c0 + lane;
+            const bool live = j < F && pw[j] > 0.0;
+            const uint64_t hit = __ballot(live && target < pre[j]);
+            const uint64_t any = __ballot(live);
+            if (hit) {
+                pick = c0 + static_cast<uint32_t>(__builtin_ctzll(hit));
+                break;
+            }
+            if (any) last = c0 + 63u - static_cast<uint32_t>(__builtin_clzll(any));
+        }
+        if (pick == kNone) pick = last;
         if (lane == 0) {
             ids[d] = lid[pick];
             lid[pick] |= kTaken;
+            pw[pick] = 0.0;
         }
     }
     return kOk;
+}
+
+// The finite scores of S[0..parents * V) in index order: ids into lid and scores into lsc
+// when there are at most kLdsCands of them, else ids into list; returns their count.
+// Wave w reads rows [w * RW, w * RW + RW) of 64 scores, lane l column l, so every load is one
+// coalesced 256-byte row, and all RW loads are in flight together.  A ballot per row and an
+// exclusive sum of the 16 waves' counts place every entry.
+template <int P>
+__device__ uint32_t finite_in_order(const float* S, uint32_t* wtot, uint32_t* lid, float* lsc, uint32_t* list) {
+    constexpr int n = P * V;
+    constexpr int RW = ((n + 63) / 64 + NWAVE - 1) / NWAVE;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    float v[RW];
+#pragma unroll
+    for (int k = 0; k < RW; ++k) v[k] = S[min((wave * RW + k) * 64 + lane, n - 1)];
+    uint64_t bal[RW];
+    uint32_t c = 0;
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+        bal[k] = __ballot((wave * RW + k) * 64 + lane < n && finite_f(v[k]));
+        c += static_cast<uint32_t>(__builtin_popcountll(bal[k]));
+    }
+    if (lane == 0) wtot[wave] = c;
+    __syncthreads();
+    uint32_t off = 0, F = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+        const uint32_t x = wtot[w];
+        off += w < wave ? x : 0u;
+        F += x;
+    }
+    const bool to_lds = F <= static_cast<uint32_t>(kLdsCands);
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[k] >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[k]), 0u));
+        if ((bal[k] >> lane) & 1u) {
+            const uint32_t pos = off + below;
+            const uint32_t i = static_cast<uint32_t>((wave * RW + k) * 64 + lane);
+            if (to_lds) {
+                lid[pos] = i;
+                lsc[pos] = v[k];
+            } else {
+                list[pos] = i;
+            }
+        }
+        off += static_cast<uint32_t>(__builtin_popcountll(bal[k]));
+    }
+    __syncthreads();
+    return F;
 }
 
 __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     __shared__ uint32_t hist[256], sel[2], wtot[NWAVE];
     __shared__ uint32_t lid[kLdsCands];
     __shared__ float lsc[kLdsCands];
+    __shared__ __align__(16) double pw[kLdsCands], pre[kLdsCands];
     __shared__ uint32_t ids[2 * kMaxBeamTake];
     __shared__ float wmax[NWAVE];
     __shared__ float mx_s;
@@ -307,23 +379,37 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
             a.status[0] = kOk;
         }
     } else {
-        // Finite entries in index order, kept in global scratch (a.list), weights in a.probs.
-        uint32_t c = 0;
-        for_each_batched(S, i0, i1, 1, [&](int, float v) { c += finite_f(v); });
+        // Finite entries in index order: in LDS (lid, lsc) when there are at most kLdsCands,
+        // else in global scratch (a.list) with the weights in a.probs.
         uint32_t F = 0;
-        uint32_t off = block_scan(c, wtot, &F);
+        switch (n / V) {
+            case 1: F = finite_in_order<1>(S, wtot, lid, lsc, a.list); break;
+            case 2: F = finite_in_order<2>(S, wtot, lid, lsc, a.list); break;
+            case 3: F = finite_in_order<3>(S, wtot, lid, lsc, a.list); break;
+            case 4: F = finite_in_order<4>(S, wtot, lid, lsc, a.list); break;
+            default: {
+                uint32_t c = 0;
+                for_each_batched(S, i0, i1, 1, [&](int, float v) { c += finite_f(v); });
+                uint32_t off = block_scan(c, wtot, &F);
+                const bool to_lds = F <= static_cast<uint32_t>(kLdsCands);
+                for_each_batched(S, i0, i1, 1, [&](int i, float v) {
+                    if (finite_f(v)) {
+                        if (to_lds) {
+                            lid[off] = static_cast<uint32_t>(i);
+                            lsc[off] = v;
+                        } else {
+                            a.list[off] = static_cast<uint32_t>(i);
+                        }
+                        ++off;
+                    }
+                });
+                __syncthreads();
+            }
+        }
         if (F <= static_cast<uint32_t>(kLdsCands)) {
-            for_each_batched(S, i0, i1, 1, [&](int i, float v) {
-                if (finite_f(v)) {
-                    lid[off] = static_cast<uint32_t>(i);
-                    lsc[off] = v;
-                    ++off;
-                }
-            });
-            __syncthreads();
             if (wave != 0) return;
             uint64_t rng = *a.rng;
-            const uint32_t st = draw_candidates_wave(lid, lsc, F, take, rng, ids);
+            const uint32_t st = draw_candidates_wave(lid, lsc, pw, pre, F, take, rng, ids);
             if (st != kOk) {
                 if (t == 0) a.status[0] = st;
                 return;
@@ -349,10 +435,6 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
             }
             return;
         }
-        for_each_batched(S, i0, i1, 1, [&](int i, float v) {
-            if (finite_f(v)) a.list[off++] = static_cast<uint32_t>(i);
-        });
-        __syncthreads();
         if (t == 0) stop_s = 0;
         uint64_t rng = *a.rng;
         for (int d = 0; d < take; ++d) {

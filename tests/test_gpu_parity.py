@@ -572,6 +572,30 @@ def test_persistent_beam_search_equals_multikernel(batch_paths, itts, opts):
     assert step.cached_tokens() == multi.cached_tokens()
 
 
+def test_step_phase_stamps(batch_paths, itts):
+    """The phase stamps of the step kernel (1 sequence) and the batch step kernel (3): every
+    phase takes a positive time, the six layer phases add up to the layer, and requests the
+    kernels cannot serve are errors.  A generate afterwards is unaffected."""
+    step, multi = batch_paths
+    for nseq in (1, 3):
+        print(f"phase stamps: nseq {nseq}", flush=True)
+        ph = step.step_phases(cached_rows=200, iters=2, nseq=nseq)
+        assert list(ph) == list(step.STEP_PHASES)
+        assert all(np.isfinite(v) and v > 0 for v in ph.values()), ph
+        parts = sum(ph[k] for k in step.STEP_PHASES[1:7])
+        assert abs(parts - ph["layer"]) <= 1e-3 * ph["layer"] + 1e-3, ph
+    for nseq in (0, 5):
+        with pytest.raises(itts.InvalidArgument):
+            step.step_phases(cached_rows=200, iters=1, nseq=nseq)
+    with pytest.raises(itts.InvalidArgument):
+        step.step_phases(cached_rows=1023, iters=1, nseq=3)
+    cond, text = itts.synthetic_prefix_inputs(30, seed=4)
+    prefix = step.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(seed=8)
+    a, b = step.generate(prefix, o, 16), multi.generate(prefix, o, 16)
+    assert (a.codes, a.stopped) == (b.codes, b.stopped)
+
+
 @pytest.mark.gpu
 def test_decoder_from_bundle_bitwise_equals_arrays(itts, small_weights, tmp_path):
     """GptDecoder.from_bundle (zero-copy from the mapping) and GptDecoder(arrays) upload the

@@ -42,9 +42,10 @@ using namespace stepc;
 template <int B>
 struct BCfg {
     static_assert(B >= 2 && B <= kStepBatchMax, "batch of the persistent batch step");
-    static constexpr int kRing = B == 2 ? 22 : B == 3 ? 18 : 14;
-    static constexpr bool kFive = false;        // five-row groups (17 chunks) need more registers than B inputs leave
-    static constexpr bool kPairs = false;       // 5120-wide rows one at a time (pairs need more registers)
+    // The staging area holds 2560 floats per sequence, so the ring keeps every mlp.c_fc and
+    // mlp.c_proj chunk of a workgroup (20 each) resident with room to prefetch.
+    static constexpr int kRing = B == 2 ? 26 : B == 3 ? 24 : 22;
+    static constexpr bool kFive = true;         // a wave's last five rows in one pass
 };
 constexpr int kResidMax = 16;  // own rows of attn.c_proj / mlp.c_proj per workgroup (grid >= 80)
 
@@ -130,12 +131,16 @@ struct PlanB {
     }
 };
 
+constexpr int kQWin = 4;    // rounds whose q / new K / new V are polled together
+constexpr int kQRec = 192;  // floats per round in the window: q, new K, new V (64 each)
+constexpr int kStageF = 2 * kWidth;  // staging floats per sequence
 template <int B>
 struct SmemB {
     union {
-        float stage[B][kFfn];                       // the phase's inputs, per sequence
+        float stage[B][kStageF];                    // the phase's inputs, per sequence
         float mpart[kAttnMaxSplits][2 + kHeadDim];  // gathered attention partials of one head (merge)
     };
+    float qwin[kQWin * kQRec];  // q / new K / new V of kQWin attention rounds
     float resid_h[B][kResidMax];  // h at this workgroup's attn.c_proj rows (their residual)
     float resid_m[B][kResidMax];  // hmid at this workgroup's mlp.c_proj rows
     float redm[4], reds[4];
@@ -160,9 +165,12 @@ __device__ __forceinline__ void chunk_src_b(const StepArgs& a, const PlanB<B>& P
         } else if (r < P.o_fc2) {
             base = wl + static_cast<size_t>(kQkv + kWidth) * kWidth + static_cast<size_t>(P.f0 + r - P.o_fc) * kWidth;
         } else {
+            // mlp.c_proj: the first two chunks of every row (activations 0-2559), then the last two
             const int q = r - P.o_fc2;
-            base = wl + static_cast<size_t>(kQkv + kWidth + kFfn) * kWidth + static_cast<size_t>(P.g0 + (q >> 2)) * kFfn +
-                   (q & 3) * kChunkF;
+            const int h = q < 2 * P.gn ? 0 : 1;
+            const int p = q - 2 * P.gn * h;
+            base = wl + static_cast<size_t>(kQkv + kWidth + kFfn) * kWidth + static_cast<size_t>(P.g0 + (p >> 1)) * kFfn +
+                   (2 * h + (p & 1)) * kChunkF;
         }
     }
     extent = kChunkF * 4;
@@ -198,8 +206,6 @@ __device__ __forceinline__ void load_rows(const float* base, const uint32_t (&of
 #pragma unroll
     for (int i = 0; i < 4; ++i) d[i] = off[i] != ~0u ? *reinterpret_cast<const float4*>(base + off[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
-constexpr int kQWin = 4;    // rounds whose q / new K / new V are polled together
-constexpr int kQRec = 192;  // floats per round in the window: q, new K, new V (64 each)
 
 // stage[q][dst + c] = LayerNorm(stage[q][src + c]) for this thread's 5 columns c = tid + 256 i
 // of each of the B staging rows.  Compute wave q (< B) forms row q's statistics with ln_stats
@@ -208,7 +214,7 @@ constexpr int kQRec = 192;  // floats per round in the window: q, new K, new V (
 // statistics itself, as the batch-1 kernel does to save the barrier, costs B times the LDS
 // reads and reductions.)
 template <int B>
-__device__ __forceinline__ void ln_stage_rows(float (*stage)[kFfn], int src, int dst, const LnPar& p, int tid, int lane,
+__device__ __forceinline__ void ln_stage_rows(float (*stage)[kStageF], int src, int dst, const LnPar& p, int tid, int lane,
                                               float (*lnst)[2], Ctl& ctl, uint32_t& gen, uint32_t* err, bool& failed) {
     static_assert(B <= kCW, "one compute wave per row's statistics");
     const int wave = tid >> 6;
@@ -311,49 +317,33 @@ __device__ __forceinline__ void gemv_rows_b(Ctl& ctl, const float* ring, int c0,
     }
 }
 
-// mlp.c_proj rows (5120 wide) for B inputs: rows k0 and, when kPairs, k0 + 4, reduced per
-// sequence with wave_sum2 (pairs: lanes 0 and 32) or wave_sum (single rows: every lane).
-template <int B, int RING, bool kPairs>
-__device__ __forceinline__ void rows_wide_b(Ctl& ctl, const float* ring, int c0, int k0, int cnt, const float (*xs)[kFfn], int wave,
-                                            int lane, uint32_t* err, bool& failed, float (&res)[B]) {
-    const bool two = kPairs && k0 + kCW < cnt;
-    release_to(ctl, c0 + 4 * k0, wave);
-    wait_run4(ctl, c0 + 4 * (two ? k0 + kCW : k0), err, failed);
-    float a0[B], a1[B];
+// Half h of mlp.c_proj row k (5120 wide): its chunks m = 2h and 2h + 1, ring chunks
+// c0 + 2 gn h + 2k and the next, times the staged half of each sequence's activations xs[q]
+// (activations 2560 h + 1280 (m - 2h) + 4 (j*64 + lane) .. + 3), added to a[q].  The two
+// calls of a row continue one FMA chain per lane in chunk order (rows_wide of step.hip).
+template <int B, int RING>
+__device__ __forceinline__ void wide_half(Ctl& ctl, const float* ring, int c, const float (*xs)[kStageF], int lane, uint32_t* err,
+                                          bool& failed, float (&a)[B]) {
 #pragma unroll
-    for (int q = 0; q < B; ++q) a0[q] = a1[q] = 0.0f;
+    for (int mm = 0; mm < 2; ++mm) {
+        const float* r0 = wait_chunk<RING>(ctl, ring, c + mm, err, failed);
+        float4 w0[5];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const float* r0 = ring + ((c0 + 4 * k0 + m) % RING) * kChunkF;
-        const float* r1 = two ? ring + ((c0 + 4 * (k0 + kCW) + m) % RING) * kChunkF : r0;
-        float4 w0[5], w1[5];
-#pragma unroll
-        for (int j = 0; j < 5; ++j) {
-            w0[j] = *reinterpret_cast<const float4*>(r0 + (j * 64 + lane) * 4);
-            if constexpr (kPairs) w1[j] = *reinterpret_cast<const float4*>(r1 + (j * 64 + lane) * 4);
-        }
+        for (int j = 0; j < 5; ++j) w0[j] = *reinterpret_cast<const float4*>(r0 + (j * 64 + lane) * 4);
 #pragma unroll
         for (int q = 0; q < B; ++q) {
             float4 x[5];
 #pragma unroll
-            for (int j = 0; j < 5; ++j) x[j] = *reinterpret_cast<const float4*>(xs[q] + ((5 * m + j) * 64 + lane) * 4);
+            for (int j = 0; j < 5; ++j) x[j] = *reinterpret_cast<const float4*>(xs[q] + ((5 * mm + j) * 64 + lane) * 4);
 #pragma unroll
             for (int j = 0; j < 5; ++j) {
-                a0[q] = __builtin_fmaf(w0[j].x, x[j].x, a0[q]);
-                a0[q] = __builtin_fmaf(w0[j].y, x[j].y, a0[q]);
-                a0[q] = __builtin_fmaf(w0[j].z, x[j].z, a0[q]);
-                a0[q] = __builtin_fmaf(w0[j].w, x[j].w, a0[q]);
-                if constexpr (kPairs) {
-                    a1[q] = __builtin_fmaf(w1[j].x, x[j].x, a1[q]);
-                    a1[q] = __builtin_fmaf(w1[j].y, x[j].y, a1[q]);
-                    a1[q] = __builtin_fmaf(w1[j].z, x[j].z, a1[q]);
-                    a1[q] = __builtin_fmaf(w1[j].w, x[j].w, a1[q]);
-                }
+                a[q] = __builtin_fmaf(w0[j].x, x[j].x, a[q]);
+                a[q] = __builtin_fmaf(w0[j].y, x[j].y, a[q]);
+                a[q] = __builtin_fmaf(w0[j].z, x[j].z, a[q]);
+                a[q] = __builtin_fmaf(w0[j].w, x[j].w, a[q]);
             }
         }
     }
-#pragma unroll
-    for (int q = 0; q < B; ++q) res[q] = kPairs ? wave_sum2(a0[q], a1[q]) : wave_sum(a0[q]);
 }
 
 constexpr int kGQkv = 1, kGProj = 1, kGFc = 2, kGHead = 3;
@@ -483,10 +473,9 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             const int g = tid >> 4, sub = tid & 15;
             const uint32_t eq = ep(l, kEpQkv), epart = ep(l, kEpPart);
             release_to(ctl, cb + P.o_att, wave);  // c_attn's rows are done: the loaders go on to c_proj
-            // The window of q / new K / new V records sits in the staging area past the two
-            // 1280-float rows (raw and normalised h) that c_attn reads, so it may be written
-            // while other waves still run c_attn.
-            float* qwin = &sm.stage[0][2 * kWidth];
+            // The window of q / new K / new V records is apart from the staging area that
+            // c_attn reads, so it may be written while other waves still run c_attn.
+            float* qwin = sm.qwin;
             // One tile's rows in registers: the next tile round's K is issued once this tile
             // round's scores are formed, its V once its weighted sum is.
             uint32_t off[4];
@@ -771,52 +760,82 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
         stamp(l, 5);
 
         // ------------------------------------------------ mlp.c_proj + residual -> next h
+        // The staging area takes half of each sequence's 5120 activations at a time: every
+        // row's first two chunks are multiplied with activations 0-2559, then its last two with
+        // 2560-5119, the accumulators carried across (the loaders stream the chunks in that
+        // order).  Up to 3 sequences, the second half's polls are in flight during the first
+        // half's products (at 4 they would not fit in registers).
         {
             const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
             const int cg = cb + P.o_fc2;
-            constexpr int NF = kFfn / kCT;
-            int idx[NF];
-            bool use[NF];
+            constexpr int NH = kFfn / kCT / 2;   // activations per thread, sequence and half
+            constexpr int RW = kResidMax / kCW;  // rows per wave at most
+            const uint32_t e = ep(l, kEpFf);
+            auto hidx = [&](int h, int (&idx)[NH]) {
 #pragma unroll
-            for (int i = 0; i < NF; ++i) {
-                idx[i] = kXff + tid + kCT * i;
-                use[i] = true;
-            }
-            // At most 40 values per thread in flight (registers): B == 2 polls both sequences'
-            // 20 at once; larger batches poll every sequence's first 10, then every
-            // sequence's last 10 (two round trips instead of one per sequence).
-            constexpr int NH = B == 2 ? NF : NF / 2;
+                for (int i = 0; i < NH; ++i) idx[i] = kXff + kStageF * h + tid + kCT * i;
+            };
+            XRead<NH> xr[B];
+            auto issue = [&](int h) {
+                int idx[NH];
+                bool use[NH];
+                hidx(h, idx);
 #pragma unroll
-            for (int h0 = 0; h0 < NF; h0 += NH) {
-                int hidx[NH];
-                bool huse[NH];
+                for (int i = 0; i < NH; ++i) use[i] = true;
 #pragma unroll
-                for (int i = 0; i < NH; ++i) {
-                    hidx[i] = idx[h0 + i];
-                    huse[i] = true;
-                }
-                XRead<NH> xr[B];
-#pragma unroll
-                for (int q = 0; q < B; ++q) xr[q].issue(XR(q), hidx, huse, ep(l, kEpFf));
+                for (int q = 0; q < B; ++q) xr[q].issue(XR(q), idx, use, e);
+            };
+            auto stage_half = [&](int h) {
+                int idx[NH];
+                hidx(h, idx);
 #pragma unroll
                 for (int q = 0; q < B; ++q) {
                     float v[NH];
-                    xr[q].wait(XR(q), hidx, ep(l, kEpFf), v, a.err, failed);
+                    xr[q].wait(XR(q), idx, e, v, a.err, failed);
 #pragma unroll
-                    for (int i = 0; i < NH; ++i) sm.stage[q][tid + kCT * (h0 + i)] = v[i];
+                    for (int i = 0; i < NH; ++i) sm.stage[q][tid + kCT * i] = v[i];
+                }
+            };
+            float acc[RW][B];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int q = 0; q < B; ++q) acc[r][q] = 0.0f;
+            constexpr bool kEarly = B <= 3;
+            issue(0);
+            stage_half(0);
+            if (kEarly) issue(1);
+            cbar(ctl, gen, a.err, failed);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (h == 1) {
+                    if (!kEarly) issue(1);
+                    cbar(ctl, gen, a.err, failed);  // every wave is past the first half's activations
+                    stage_half(1);
+                    cbar(ctl, gen, a.err, failed);
+                }
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const int k = wave + kCW * r;
+                    if (k < P.gn) {
+                        const int c = cg + 2 * P.gn * h + 2 * k;
+                        release_to(ctl, c, wave);
+                        wide_half<B, RING>(ctl, ring, c, sm.stage, lane, a.err, failed, acc[r]);
+                    }
                 }
             }
-            cbar(ctl, gen, a.err, failed);
-            const int step_k = C::kPairs ? 8 : 4;
-            for (int k0 = wave; k0 < P.gn; k0 += step_k) {
-                float res[B];
-                rows_wide_b<B, RING, C::kPairs>(ctl, ring, cg, k0, P.gn, sm.stage, wave, lane, a.err, failed, res);
-                const int k = C::kPairs ? k0 + 4 * (lane >> 5) : k0;
-                const bool holder = C::kPairs ? (lane & 31) == 0 : lane == 0;
-                if (holder && k < P.gn) {
-                    const float b = par[kParFc2B + P.g0 + k];
 #pragma unroll
-                    for (int q = 0; q < B; ++q) xst_bcast(XW(q), kXh + P.g0 + k, ep(l + 1, kEpXh), sm.resid_m[q][k] + (res[q] + b));
+            for (int r = 0; r < RW; ++r) {
+                const int k = wave + kCW * r;
+                if (k < P.gn) {
+                    float res[B];
+#pragma unroll
+                    for (int q = 0; q < B; ++q) res[q] = wave_sum(acc[r][q]);
+                    if (lane == 0) {
+                        const float b = par[kParFc2B + P.g0 + k];
+#pragma unroll
+                        for (int q = 0; q < B; ++q) xst_bcast(XW(q), kXh + P.g0 + k, ep(l + 1, kEpXh), sm.resid_m[q][k] + (res[q] + b));
+                    }
                 }
             }
             release_to(ctl, (l + 1) * P.layer_chunks, wave);
@@ -855,14 +874,15 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             for (int i = 0; i < 5; ++i) sm.stage[q][tid + 256 * i] = hv[i];
         }
         cbar(ctl, gen, a.err, failed);
-        // ln_f, then final_norm, each into the next 1280 floats of the sequence's staging row
+        // ln_f into the second 1280 floats of the sequence's staging row, then final_norm back
+        // into the first (the raw row is no longer read)
         ln_stage_rows<B>(sm.stage, 0, kWidth, lf, tid, lane, sm.lnst, ctl, gen, a.err, failed);
         cbar(ctl, gen, a.err, failed);
-        ln_stage_rows<B>(sm.stage, kWidth, 2 * kWidth, fn, tid, lane, sm.lnst, ctl, gen, a.err, failed);
+        ln_stage_rows<B>(sm.stage, kWidth, 0, fn, tid, lane, sm.lnst, ctl, gen, a.err, failed);
         cbar(ctl, gen, a.err, failed);
         const float* x[B];
 #pragma unroll
-        for (int q = 0; q < B; ++q) x[q] = sm.stage[q] + 2 * kWidth;
+        for (int q = 0; q < B; ++q) x[q] = sm.stage[q];
         auto out = [&](int k, float b, int q, float acc) { a.logits[static_cast<size_t>(q) * a.logit_stride + P.h0 + k] = acc + b; };
         gemv_rows_b<B, RING, C::kFive>(ctl, ring, chd, P.hn, x, bias, a.head + kHeadBias + P.h0, wave, lane, a.err, failed, out);
         release_to(ctl, total_chunks, wave);

@@ -11,9 +11,10 @@
 //   replacement with sample_gpt_token_from_logits (:217-222), by wave 0 alone with the
 //   finite candidates in LDS when there are at most kLdsCands of them (each draw's sums
 //   lane-serial in index order); then a stable sort of the candidates by score (:228).
-// beam_children_kernel picks the children on the device (the next forward is queued without
-// waiting for the host); the host reads the candidates a step or two later and runs the
-// reference's child/finish bookkeeping.
+// beam_advance_kernel picks the children on the device (the next forward is queued without
+// waiting for the host) and reorders their row owners and repetition sets; the host reads
+// the candidates (written into pinned memory by beam_select_kernel) a step or two later and
+// runs the reference's child/finish bookkeeping.
 #include "sampler_dev.h"
 
 namespace itts {
@@ -331,7 +332,7 @@ __device__ uint32_t finite_in_order(const float* S, uint32_t* wtot, uint32_t* li
     return F;
 }
 
-__global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
+__device__ __forceinline__ void select_candidates(const BeamArgs& a) {
     __shared__ uint32_t hist[256], sel[2], wtot[NWAVE];
     __shared__ uint32_t lid[kLdsCands];
     __shared__ float lsc[kLdsCands];
@@ -514,49 +515,106 @@ __global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
     }
 }
 
-// One thread: at most 2 * 10 candidates and 10 children.
-__global__ void beam_children_kernel(const BeamCand* cand, int take, int beams, uint32_t* parents_dev, uint32_t* parent, uint32_t* token,
-                                     float* score, SeqState* state, const SeqState* tmpl, uint32_t n, uint32_t position) {
-    if (threadIdx.x != 0) return;
-    const uint32_t P = *parents_dev;
-    int C = 0;
-    for (int r = 0; r < take && C < beams; ++r) {
-        const BeamCand c = cand[r];
-        if (c.token == static_cast<uint32_t>(kMelStop)) continue;
-        if (c.token >= static_cast<uint32_t>(kMelStart) || c.parent >= P) {
-            C = 0;
-            break;
+// The selection, then (when a.host_cand is set) its candidates and every status of the step
+// copied into pinned host memory, so the host needs no copy launches to read them.  Every
+// thread returns from select_candidates before the barrier.
+__global__ __launch_bounds__(NT) void beam_select_kernel(BeamArgs a) {
+    select_candidates(a);
+    if (!a.host_cand) return;
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < a.take) a.host_cand[t] = a.cand[t];
+    if (t <= a.parents) a.host_status[t] = a.status[t];
+}
+
+// dst[0..bytes) = src[0..bytes) by the workgroup, 16 bytes per thread and step (both
+// buffers 16-byte aligned, not overlapping).
+__device__ __forceinline__ void copy_block(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, uint32_t bytes) {
+    const uint32_t n16 = bytes / 16;
+    const uint4* s16 = reinterpret_cast<const uint4*>(src);
+    uint4* d16 = reinterpret_cast<uint4*>(dst);
+    for (uint32_t i = threadIdx.x; i < n16; i += NT) d16[i] = s16[i];
+    for (uint32_t i = n16 * 16 + threadIdx.x; i < bytes; i += NT) dst[i] = src[i];
+}
+
+// Children (thread 0; at most 2 * 10 candidates and 10 children), then the reorder by the
+// whole workgroup: the first `beams` repetition sets and table rows (each a contiguous block)
+// are staged, then each child's written from its parent's.  A repetition set (8194 bytes,
+// rows 2-byte aligned) is copied in 2-byte pieces, the child's token set in its piece.
+__global__ __launch_bounds__(NT) void beam_advance_kernel(BeamAdvanceArgs a) {
+    __shared__ uint32_t par_s[kMaxBatch], tok_s[kMaxBatch];
+    const int t = threadIdx.x;
+    const int beams = a.beams;
+    if (t == 0) {
+        const uint32_t P = *a.parents_dev;
+        int C = 0;
+        for (int r = 0; r < a.take && C < beams; ++r) {
+            const BeamCand c = a.cand[r];
+            if (c.token == static_cast<uint32_t>(kMelStop)) continue;
+            if (c.token >= static_cast<uint32_t>(kMelStart) || c.parent >= P) {
+                C = 0;
+                break;
+            }
+            par_s[C] = c.parent;
+            tok_s[C] = c.token;
+            a.score[C] = c.score;
+            ++C;
         }
-        parent[C] = c.parent;
-        token[C] = c.token;
-        score[C] = c.score;
-        ++C;
+        for (int c = 0; c < beams; ++c) {
+            SeqState st = *a.tmpl;
+            st.n = a.n;
+            st.position = a.position;
+            if (c < C) {
+                st.token = tok_s[c];
+            } else {
+                par_s[c] = 0;
+                tok_s[c] = 0;
+                a.score[c] = -INFINITY;
+                st.token = 0;
+                st.active = 0;
+            }
+            a.parent[c] = par_s[c];
+            a.token[c] = tok_s[c];
+            a.state[c] = st;
+        }
+        *a.parents_dev = C > 0 ? static_cast<uint32_t>(C) : 1u;
     }
+    const uint32_t n = a.n, cap = a.cap;
+    copy_block(a.seen_tmp, a.seen, static_cast<uint32_t>(beams) * V);
+    copy_block(a.table_tmp, a.table, static_cast<uint32_t>(beams) * cap);
+    __syncthreads();  // the staged rows, par_s and tok_s are seen by the whole workgroup
+    static_assert(V % 2 == 0, "repetition sets in 2-byte pieces");
+    constexpr uint32_t kHalf = V / 2;
     for (int c = 0; c < beams; ++c) {
-        SeqState st = *tmpl;
-        st.n = n;
-        st.position = position;
-        if (c < C) {
-            st.token = token[c];
-        } else {
-            parent[c] = 0;
-            token[c] = 0;
-            score[c] = -INFINITY;
-            st.token = 0;
-            st.active = 0;
+        const uint32_t p = par_s[c], tk = tok_s[c];
+        const uint16_t* __restrict__ src = reinterpret_cast<const uint16_t*>(a.seen_tmp + static_cast<size_t>(p) * V);
+        uint16_t* __restrict__ dst = reinterpret_cast<uint16_t*>(a.seen + static_cast<size_t>(c) * V);
+        uint16_t v[(kHalf + NT - 1) / NT];
+#pragma unroll
+        for (int u = 0; u < (kHalf + NT - 1) / NT; ++u) {
+            const uint32_t j = t + u * NT;
+            v[u] = j < kHalf ? src[j] : 0;
         }
-        state[c] = st;
+#pragma unroll
+        for (int u = 0; u < (kHalf + NT - 1) / NT; ++u) {
+            const uint32_t j = t + u * NT;
+            if (j < kHalf) {
+                uint16_t x = v[u];
+                if (j == tk >> 1) x = (tk & 1u) ? static_cast<uint16_t>((x & 0x00ffu) | 0x0100u) : static_cast<uint16_t>((x & 0xff00u) | 0x0001u);
+                dst[j] = x;
+            }
+        }
+        const uint8_t* __restrict__ ts = a.table_tmp + static_cast<size_t>(p) * cap;
+        uint8_t* __restrict__ td = a.table + static_cast<size_t>(c) * cap;
+        for (uint32_t r = t; r <= n; r += NT) td[r] = r == n ? static_cast<uint8_t>(c) : ts[r];
     }
-    *parents_dev = C > 0 ? static_cast<uint32_t>(C) : 1u;
 }
 
 }  // namespace
 
-hipError_t launch_beam_children(const BeamCand* cand, int take, int beams, uint32_t* parents_dev, uint32_t* parent, uint32_t* token,
-                                float* score, SeqState* state, const SeqState* tmpl, uint32_t n, uint32_t position, hipStream_t s) {
-    if (take < 1 || take > kMaxBeamTake || beams < 1 || beams > kMaxBatch) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(beam_children_kernel, dim3(1), dim3(64), 0, s, cand, take, beams, parents_dev, parent, token, score, state, tmpl, n,
-                       position);
+hipError_t launch_beam_advance(const BeamAdvanceArgs& a, hipStream_t s) {
+    if (a.take < 1 || a.take > kMaxBeamTake || a.beams < 1 || a.beams > kMaxBatch || a.n + 1 > a.cap) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(beam_advance_kernel, dim3(1), dim3(NT), 0, s, a);
     return hipGetLastError();
 }
 

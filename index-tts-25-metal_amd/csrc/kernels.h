@@ -193,18 +193,34 @@ struct BeamArgs {
     float temperature, top_p, penalty;
     uint32_t top_k, num_beams;
     const uint32_t* parents_dev;  // the step's parent count on the device (<= parents), or null: parents
+    BeamCand* host_cand;          // pinned host copies of cand[0..take) and status[0..parents], written
+    uint32_t* host_status;        // by beam_select once it is done (null: none)
 };
 hipError_t launch_beam_scores(const BeamArgs& a, hipStream_t s);
 hipError_t launch_beam_select(const BeamArgs& a, hipStream_t s);
-// Children of a beam step on the device (gpt_sampling.cpp:229-236): from the ranked
-// candidates, skipping stop tokens, the first `beams` become children 0, 1, ... with
-// parent[c], token[c], score[c] (the next step's parent scores) and state[c] (tmpl with
-// n, position and token[c]).  Slots without a child, and every slot when a candidate is out
-// of range (a code >= 8192 or a parent >= *parents_dev: the host raises at that step), are
-// inactive with parent 0 and token 0.  *parents_dev becomes the child count, at least 1.
-hipError_t launch_beam_children(const BeamCand* cand, int take, int beams, uint32_t* parents_dev, uint32_t* parent,
-                                uint32_t* token, float* score, SeqState* state, const SeqState* tmpl, uint32_t n, uint32_t position,
-                                hipStream_t s);
+// Children of a beam step on the device (gpt_sampling.cpp:229-236), then the reorder of
+// their cached rows' owners and repetition sets, in one launch.
+// - Children: from the ranked candidates, skipping stop tokens, the first `beams` become
+//   children 0, 1, ... with parent[c], token[c], score[c] (the next step's parent scores)
+//   and state[c] (tmpl with n, position and token[c]).  Slots without a child, and every
+//   slot when a candidate is out of range (a code >= 8192 or a parent >= *parents_dev: the
+//   host raises at that step), are inactive with parent 0 and token 0.  *parents_dev
+//   becomes the child count, at least 1.
+// - Reorder: every slot's table row (rows 0..n-1) and repetition set are staged, then child
+//   c takes parent[c]'s, owns row n itself and adds token[c] to its set.
+struct BeamAdvanceArgs {
+    const BeamCand* cand;
+    int take, beams;
+    uint32_t* parents_dev;
+    uint32_t *parent, *token;
+    float* score;
+    SeqState* state;
+    const SeqState* tmpl;
+    uint32_t n, position, cap;
+    uint8_t *table, *table_tmp;  // [beams][cap] row owners
+    uint8_t *seen, *seen_tmp;    // [beams][8194] repetition sets
+};
+hipError_t launch_beam_advance(const BeamAdvanceArgs& a, hipStream_t s);
 
 // ------------------------------------------------------------------ prefill
 struct LnRowsArgs {
@@ -281,10 +297,5 @@ hipError_t launch_seen_reset(uint8_t* seen, int nseq, hipStream_t s);
 hipError_t launch_prefill_rows_one(uint32_t* row_slot, uint32_t* row_pos, uint32_t* last_rows, uint32_t rows, hipStream_t s);
 // Copy row src_rows[b] of x into h[b] (last prefix row of each sequence).
 hipError_t launch_gather_rows(const float* x, const uint32_t* src_rows, float* h, int batch, hipStream_t s);
-// Beam reorder: child c (of `children`) takes parent[c]'s row owners for rows 0..n-1 and its
-// repetition set plus token[c]; it owns row n itself.  `parents` rows are staged first, so
-// several children may share a parent.
-hipError_t launch_beam_reorder(uint8_t* table, uint8_t* table_tmp, uint8_t* seen, uint8_t* seen_tmp, const uint32_t* parent,
-                               const uint32_t* token, int parents, int children, uint32_t n, uint32_t cap, hipStream_t s);
 
 }  // namespace itts

@@ -227,16 +227,17 @@ struct Engine {
     DevBuf<double> beam_probs;
     DevBuf<BeamCand> cand;
     DevBuf<uint64_t> beam_rng;
-    DevBuf<uint32_t> beam_np;    // the step's parent count, advanced by beam_children_kernel
+    DevBuf<uint32_t> beam_np;    // the step's parent count, advanced by beam_advance_kernel
     DevBuf<SeqState> beam_tmpl;  // decode state of a child, before its n, position and token
-    // Candidates and statuses of a queued beam step, read back into pinned memory; the host
-    // runs up to kBeamLag steps behind the device.
+    // Candidates and statuses of a queued beam step, written into pinned memory by
+    // beam_select_kernel; the host runs up to kBeamLag steps behind the device.
     struct BeamSlot {
         BeamCand cand[kMaxBeamTake];
         uint32_t status[1 + kMaxBatch];
     };
     static constexpr uint32_t kBeamRing = 4, kBeamLag = 2;
     BeamSlot* beam_ring = nullptr;
+    BeamSlot* beam_ring_dev = nullptr;  // beam_ring as the device addresses it
     hipEvent_t bev[kBeamRing] = {};
     // API scratch
     DevBuf<float> api_out;
@@ -1420,10 +1421,11 @@ void Engine::generate_segments(const float* cond, uint32_t n_cond, const float* 
 }
 
 // gpt_sampling.cpp:190-245.  Scores, processors and candidate selection run on the device
-// (beam.hip); so does the choice of children (beam_children_kernel applies the rule of
+// (beam.hip); so does the choice of children (beam_advance_kernel applies the rule of
 // :229-236 to the ranked candidates), so every step (scores, selection, children, KV
 // reorder, forward) is queued without waiting for the host.  The host reads each step's
-// candidates back a step or two later and runs the reference's child/finish bookkeeping
+// candidates (written into pinned memory by the selection) a step or two later and runs
+// the reference's child/finish bookkeeping
 // on them, with the same rule, so its beams are the device's children.  When the search
 // ends (early stop, no children, an error), up to kBeamLag queued steps are discarded.
 // Beam KV is not snapshotted: child c lives in slot c and inherits its parent's rows
@@ -1456,6 +1458,7 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
     beam_tmpl.ensure(1);
     if (!beam_ring) {
         HIP_CHECK(hipHostMalloc(&beam_ring, kBeamRing * sizeof(BeamSlot), hipHostMallocDefault));
+        HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&beam_ring_dev), beam_ring, 0));
         for (auto& e : bev) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     const int nb = gemv_batch_bucket(static_cast<int>(nbeam));
@@ -1506,17 +1509,30 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
         a.penalty = config.repetition_penalty;
         a.top_k = config.top_k;
         a.num_beams = nbeam;
+        BeamSlot& slot = beam_ring_dev[k % kBeamRing];
+        a.host_cand = slot.cand;
+        a.host_status = slot.status;
         HIP_CHECK(launch_beam_scores(a, stream));
         HIP_CHECK(launch_beam_select(a, stream));
-        BeamSlot& slot = beam_ring[k % kBeamRing];
-        HIP_CHECK(hipMemcpyAsync(slot.cand, cand.p, take * sizeof(BeamCand), hipMemcpyDeviceToHost, stream));
-        HIP_CHECK(hipMemcpyAsync(slot.status, status.p, (1 + nbeam) * 4, hipMemcpyDeviceToHost, stream));
         if (k + 1 < maximum) {
-            const uint32_t n = rows + k;  // rows cached before this forward, equal for every beam
-            HIP_CHECK(launch_beam_children(cand.p, static_cast<int>(take), static_cast<int>(nbeam), beam_np.p, d_parent.p, d_token.p,
-                                           beam_scores.p, state.p, beam_tmpl.p, n, k + 2, stream));
-            HIP_CHECK(launch_beam_reorder(table.p, table_tmp.p, seen.p, seen_tmp.p, d_parent.p, d_token.p, static_cast<int>(nbeam),
-                                          static_cast<int>(nbeam), n, cap, stream));
+            BeamAdvanceArgs v{};
+            v.cand = cand.p;
+            v.take = static_cast<int>(take);
+            v.beams = static_cast<int>(nbeam);
+            v.parents_dev = beam_np.p;
+            v.parent = d_parent.p;
+            v.token = d_token.p;
+            v.score = beam_scores.p;
+            v.state = state.p;
+            v.tmpl = beam_tmpl.p;
+            v.n = rows + k;  // rows cached before this forward, equal for every beam
+            v.position = k + 2;
+            v.cap = cap;
+            v.table = table.p;
+            v.table_tmp = table_tmp.p;
+            v.seen = seen.p;
+            v.seen_tmp = seen_tmp.p;
+            HIP_CHECK(launch_beam_advance(v, stream));
             run_step(static_cast<int>(nbeam), nb, false, true);
         }
         HIP_CHECK(hipEventRecord(bev[k % kBeamRing], stream));

@@ -76,24 +76,6 @@ __global__ void gather_rows_kernel(const float* x, const uint32_t* src_rows, flo
 
 // Beam reorder: child c inherits parent[c]'s row owners (rows 0..n-1) and repetition set
 // (plus its new token) and owns row n itself.  Parents are staged first so children may share them.
-__global__ void beam_stage_kernel(const uint8_t* table, uint8_t* table_tmp, const uint8_t* seen, uint8_t* seen_tmp, uint32_t n,
-                                  uint32_t cap) {
-    const int b = blockIdx.y;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        table_tmp[static_cast<size_t>(b) * cap + i] = table[static_cast<size_t>(b) * cap + i];
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < static_cast<uint32_t>(kMelVocab); i += gridDim.x * blockDim.x)
-        seen_tmp[static_cast<size_t>(b) * kMelVocab + i] = seen[static_cast<size_t>(b) * kMelVocab + i];
-}
-__global__ void beam_apply_kernel(uint8_t* table, const uint8_t* table_tmp, uint8_t* seen, const uint8_t* seen_tmp,
-                                  const uint32_t* parent, const uint32_t* token, uint32_t n, uint32_t cap) {
-    const int c = blockIdx.y;
-    const uint32_t p = parent[c], tok = token[c];
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i <= n; i += gridDim.x * blockDim.x)
-        table[static_cast<size_t>(c) * cap + i] = i == n ? static_cast<uint8_t>(c) : table_tmp[static_cast<size_t>(p) * cap + i];
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < static_cast<uint32_t>(kMelVocab); i += gridDim.x * blockDim.x)
-        seen[static_cast<size_t>(c) * kMelVocab + i] = i == tok ? 1 : seen_tmp[static_cast<size_t>(p) * kMelVocab + i];
-}
-
 // Repetition sets of sequences 0..grid.y-1: exactly {1, 8192} (gpt_sampling.cpp:176).
 __global__ void seen_reset_kernel(uint8_t* seen) {
     uint8_t* row = seen + static_cast<size_t>(blockIdx.y) * kMelVocab;
@@ -158,13 +140,6 @@ hipError_t launch_speaker_row(const float* w, const float* b, const float* speak
 
 hipError_t launch_gather_rows(const float* x, const uint32_t* src_rows, float* h, int batch, hipStream_t s) {
     hipLaunchKernelGGL(gather_rows_kernel, dim3(batch), dim3(256), 0, s, x, src_rows, h);
-    return hipGetLastError();
-}
-
-hipError_t launch_beam_reorder(uint8_t* table, uint8_t* table_tmp, uint8_t* seen, uint8_t* seen_tmp, const uint32_t* parent,
-                               const uint32_t* token, int parents, int children, uint32_t n, uint32_t cap, hipStream_t s) {
-    hipLaunchKernelGGL(beam_stage_kernel, dim3(8, parents), dim3(256), 0, s, table, table_tmp, seen, seen_tmp, n, cap);
-    hipLaunchKernelGGL(beam_apply_kernel, dim3(8, children), dim3(256), 0, s, table, table_tmp, seen, seen_tmp, parent, token, n, cap);
     return hipGetLastError();
 }
 

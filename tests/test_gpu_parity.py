@@ -352,6 +352,9 @@ def beam_small(itts, oracle, small_weights):
     dict(do_sample=True, seed=7, num_beams=3),
     dict(do_sample=True, seed=9, num_beams=2, top_k=0, top_p=0.9, temperature=1.2),
     dict(do_sample=False, num_beams=4, length_penalty=1.0, top_k=5),
+    # every score but the two suppressed codes finite (8192 per parent): the selection keeps
+    # its 24576 candidates in global memory instead of LDS
+    dict(do_sample=True, seed=11, num_beams=3, top_k=0, top_p=1.0, temperature=1.0, repetition_penalty=1.0, suppress_stop=True),
 ])
 def test_beam_search_matches_oracle(beam_small, itts, oracle, opts):
     dec, orc, prefix = beam_small

@@ -264,6 +264,11 @@ int itts_codec_bench(itts_codec* c, uint32_t n, uint32_t iters, float* avg_ms, d
 #define ITTS_LIBM_EXP 1
 #define ITTS_LIBM_LOGF 2
 int itts_libm_eval(int32_t fn, uint64_t first_bits, uint64_t stride, uint64_t count, void* out);
+/* Verification hook (no reference counterpart): out[r] = the float sum, in index order, of
+ * row r of values (rows x 8194 floats, each >= 0 or NaN), as the beam scores form the
+ * log-softmax denominator (gpt_sampling.cpp:208), with the same device code.  values and
+ * out are host memory; rows <= 65536. */
+int itts_chain_sum_eval(const float* values, uint32_t rows, float* out);
 
 /* Deterministic N(mean, std^2) fill for synthetic weights and inputs: value i is
  * a Box-Muller transform of two SplitMix64 outputs keyed by (seed, i), so the

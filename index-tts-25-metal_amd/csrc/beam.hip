@@ -2,8 +2,8 @@
 //
 // beam_scores_kernel, one 1024-thread workgroup per parent beam:
 //   log_probs = logits - (peak + log(sum_i exp(logit_i - peak)))   (:207-210, float; the
-//   sum is formed by one lane in index order from 16-byte LDS reads issued a chunk ahead,
-//   expf/logf bit for bit those of glibc (glibc_math.h)), then the processors with the
+//   sum is the reference's index-order float chain bit for bit, formed by one wave
+//   (chain_sum.h); expf/logf bit for bit those of glibc (glibc_math.h)), then the processors with the
 //   parent's repetition set (:211-212), then + the parent's beam score (:213).
 // beam_select_kernel, one workgroup:
 //   greedy: the take = 2*beams best of all parents' scores by (score desc, index asc)
@@ -15,6 +15,7 @@
 // waiting for the host) and reorders their row owners and repetition sets; the host reads
 // the candidates (written into pinned memory by beam_select_kernel) a step or two later and
 // runs the reference's child/finish bookkeeping.
+#include "chain_sum.h"
 #include "sampler_dev.h"
 
 namespace itts {
@@ -33,6 +34,7 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     }
     const float* lg = a.logits + static_cast<size_t>(p) * V;
     float* e = reinterpret_cast<float*>(sm.sortbuf) + V + 2;  // after s[] inside the union, 16-byte aligned
+    static_assert(V + 2 + chain::kPad <= kSortMax * 2, "the padded exponentials fit in the sort buffer");
     float mloc = -INFINITY;
     {
         float v[IPT];  // all loads in flight before the first store
@@ -57,42 +59,11 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     float peak = wred[0];
     for (int w = 1; w < NWAVE; ++w) peak = fmaxf(peak, wred[w]);
     for (int i = t; i < V; i += NT) e[i] = libm::expf_glibc(sm.s[i] - peak);
+    for (int i = V + t; i < chain::kPad; i += NT) e[i] = 0.0f;  // adding +0 leaves the sum unchanged
     __syncthreads();
-    if (t == 0) {
-        // sum += e[0], e[1], ... in index order; the next 32 values are read while the
-        // current 32 are added
-        constexpr int kQuads = V / 4;  // 2048: 8192 values, then the last V % 4
-        constexpr int kQ = 8;          // quads per register chunk
-        static_assert(kQuads % (2 * kQ) == 0, "two chunks of kQ quads per iteration");
-        const float4* e4 = reinterpret_cast<const float4*>(e);
-        float sum = 0.0f;
-        float4 c0[kQ], c1[kQ];
-#pragma unroll
-        for (int k = 0; k < kQ; ++k) c0[k] = e4[k];
-        for (int q0 = 0; q0 < kQuads; q0 += 2 * kQ) {
-#pragma unroll
-            for (int k = 0; k < kQ; ++k) c1[k] = e4[q0 + kQ + k];
-#pragma unroll
-            for (int k = 0; k < kQ; ++k) {
-                sum += c0[k].x;
-                sum += c0[k].y;
-                sum += c0[k].z;
-                sum += c0[k].w;
-            }
-            if (q0 + 2 * kQ < kQuads) {
-#pragma unroll
-                for (int k = 0; k < kQ; ++k) c0[k] = e4[q0 + 2 * kQ + k];
-            }
-#pragma unroll
-            for (int k = 0; k < kQ; ++k) {
-                sum += c1[k].x;
-                sum += c1[k].y;
-                sum += c1[k].z;
-                sum += c1[k].w;
-            }
-        }
-        for (int i = kQuads * 4; i < V; ++i) sum += e[i];
-        log_sum_s = peak + libm::logf_glibc(sum);
+    if (wave == 0) {
+        const float sum = chain::sum_wave(e, lane);
+        if (lane == 0) log_sum_s = peak + libm::logf_glibc(sum);
     }
     __syncthreads();
     const float log_sum = log_sum_s;

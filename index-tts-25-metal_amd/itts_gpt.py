@@ -127,6 +127,7 @@ def _load() -> C.CDLL:
         "itts_codec_decode": (C.c_int, [P, u32p, u32, f32p]),
         "itts_codec_bench": (C.c_int, [P, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_double)]),
         "itts_libm_eval": (C.c_int, [i32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_void_p]),
+        "itts_chain_sum_eval": (C.c_int, [C.POINTER(C.c_float), u32, C.POINTER(C.c_float)]),
         "itts_qwen_create": (C.c_int, [C.POINTER(_Tensor), i32, C.POINTER(_QwenConfig), C.POINTER(P)]),
         "itts_qwen_create_from_bundle": (C.c_int, [P, C.POINTER(_QwenConfig), C.POINTER(P)]),
         "itts_qwen_destroy": (None, [P]),

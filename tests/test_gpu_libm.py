@@ -68,3 +68,61 @@ def test_strided_all_bit_patterns(itts, oracle, fn, name):
     checked, bad = _compare(itts, oracle, fn, 0, 61, (1 << 32) // 61)
     print(f"{name}: {bad} of {checked} strided bit patterns differ from glibc", flush=True)
     assert bad == 0
+
+
+def _chain_rows(seed):
+    """Rows of 8194 non-negative floats: exp(x - max) of logit rows of several spreads, masked
+    and tied logits, all-equal rows, sums that start subnormal, and tie-heavy sequences of
+    short-mantissa powers of two (which put exact halves of the running sum's unit in play)."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for sd in (0.5, 1.0, 3.0, 10.0, 40.0):
+        x = rng.standard_normal(8194) * sd
+        rows.append(x)
+        rows.append(np.round(x * 4) / 4)
+        m = x.copy()
+        m[rng.random(8194) < 0.4] = -np.inf
+        rows.append(m)
+    rows.append(np.zeros(8194))
+    rows.append(-100.0 + rng.standard_normal(8194))
+    out = []
+    for x in rows:
+        x = x.astype(np.float32)
+        out.append(np.exp(x - x.max()).astype(np.float32))
+    tiny = out[-1].copy()
+    tiny[4000] = 1.0
+    out.append(tiny)
+    # subnormal exponentials: a running sum that stays below 2^-126 for 8000 values
+    for lo in (-95.0, -101.0):
+        x = (lo + rng.standard_normal(8194) * 0.5).astype(np.float32)
+        x[8000] = 0.0
+        e = np.exp(x.astype(np.float64)).astype(np.float32)
+        assert np.count_nonzero((e > 0) & (e < np.finfo(np.float32).tiny)) > 4000
+        out.append(e)
+    for _ in range(12):
+        ex = -rng.integers(0, 40, 8194)
+        v = np.ldexp(1.0 + rng.integers(0, 4, 8194) * 0.25, ex).astype(np.float32)
+        v[rng.random(8194) < 0.2] = 0.0
+        out.append(v)
+    return np.stack(out)
+
+
+def test_beam_softmax_sum_is_the_index_order_chain(itts):
+    """The beam scores' log-softmax denominator (gpt_sampling.cpp:208: sum += exp(value - peak)
+    in index order, float) is formed on the device without 8194 dependent additions
+    (csrc/chain_sum.h).  It must equal the one-at-a-time float chain bit for bit; the chain is
+    numpy's sequential float32 accumulate, itself checked against a Python loop on one row."""
+    vals = _chain_rows(5)
+    exp = np.add.accumulate(vals, axis=1, dtype=np.float32)[:, -1]
+    s = np.float32(0.0)
+    for v in vals[7]:
+        s = np.float32(s + v)
+    assert s.view(np.uint32) == exp[7].view(np.uint32)
+    got = np.empty(len(vals), np.float32)
+    v = np.ascontiguousarray(vals)
+    st = itts._lib.itts_chain_sum_eval(v.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(vals),
+                                       got.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    assert st == 0
+    bad = np.nonzero(got.view(np.uint32) != exp.view(np.uint32))[0]
+    print(f"chain sum: {len(bad)} of {len(vals)} rows differ", flush=True)
+    assert len(bad) == 0, [(int(i), float(got[i]), float(exp[i])) for i in bad[:5]]

@@ -30,10 +30,8 @@ namespace {
 
 constexpr int kNW = 4;  // waves per GEMV workgroup
 
-// Splits actually used for L keys: about kAttnSplitRows rows each, at most `max_splits`.
-__device__ __forceinline__ int live_splits(int L, int max_splits) {
-    return min(max_splits, max(1, (L + kAttnSplitRows - 1) / kAttnSplitRows));
-}
+// Splits actually used for L keys (attn_splits).
+__device__ __forceinline__ int live_splits(int L, int max_splits) { return attn_splits(L, max_splits); }
 
 // The prologue of a batched GEMV, once per sequence: xn[b] = LayerNorm(s) of sequence b's
 // input row (kProEmbedLn: of h = mel_emb[token] + mel_pos[position], also written to h_out).

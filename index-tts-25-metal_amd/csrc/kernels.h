@@ -79,8 +79,21 @@ struct AttnArgs {
     int splits;
 };
 constexpr int kAttnMaxChunk = 128;   // rows per split at most
-constexpr int kAttnSplitRows = 64;   // target rows per split
+constexpr int kAttnSplitRows = 64;   // target rows per split, up to kAttnRoundSplits splits
 constexpr int kAttnMaxSplits = 64;   // splits per (sequence, head) at most
+constexpr int kAttnRoundSplits = 12;  // 20 heads x 12 splits: one round of a 256-workgroup grid
+// Splits of the attention over L keys (at most max_splits, which the host sizes so that no
+// split exceeds kAttnMaxChunk rows): about kAttnSplitRows rows each while that takes at most
+// kAttnRoundSplits splits, else kAttnRoundSplits splits or, past 12 * 128 keys, splits of up
+// to kAttnMaxChunk rows.  Every attention path (decode.hip, step.hip, step_batch.hip) uses
+// this rule, so their tiles and merges are the same.
+__host__ __device__ inline int attn_splits(int L, int max_splits) {
+    const int fine = (L + kAttnSplitRows - 1) / kAttnSplitRows;
+    const int coarse = (L + kAttnMaxChunk - 1) / kAttnMaxChunk;
+    int s = fine <= kAttnRoundSplits ? fine : (coarse > kAttnRoundSplits ? coarse : kAttnRoundSplits);
+    if (s < 1) s = 1;
+    return s < max_splits ? s : max_splits;
+}
 // Split pass (kAttnGrid workgroups walking the live (sequence, split, head) tiles) then
 // merge pass (grid 20 x batch).
 constexpr int kAttnGrid = 1024;

@@ -457,8 +457,8 @@ struct Engine {
 
     // The persistent step runs when one 512-thread workgroup fits per CU (the grid is one
     // workgroup per CU, all resident together), there is a workgroup per attention head
-    // (step_fits: head h's merge runs on workgroup h), weights are FP32 and attention
-    // tiles stay <= 64 rows (cap <= 4096).
+    // (step_fits: head h's merge runs on workgroup h), weights are FP32 and the cache holds
+    // at most 4096 rows (at most 32 splits, kAttnMaxChunk rows each).
     void init_step() {
         const char* pe = std::getenv("ITTS_GPT_PERSISTENT");
         if ((pe && std::strcmp(pe, "0") == 0) || bf16 || cap > 4096) return;

@@ -549,11 +549,11 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 const bool act = P.tile(rd, h, s, t0, R);
                 const int p1 = act ? min(P.L, t0 + P.chunk_rows) : 0;
                 const int kc = act ? Plan::kv_chunks(R) : 0;
-                // 8 arithmetic slots as attention_kernel; a tile has <= 64 rows here (KV capacity
-                // <= 4096, checked on the host), so only slots 0..3 can hold a row and slots
-                // 4..7 stay constant zeros (-inf scores) exactly as in the multi-kernel path.
+                // 8 arithmetic slots as attention_kernel (rows g + 16 i of a tile of up to
+                // kAttnMaxChunk rows); slots past the tile's rows are zeros with -inf scores,
+                // exactly as in the multi-kernel path.
                 constexpr int PER = kAttnMaxChunk / 16;
-                constexpr int PERL = 4;
+                constexpr int PERL = PER;
                 float4 k4[PER], v4[PER];
 #pragma unroll
                 for (int i = 0; i < PER; ++i) {

@@ -181,16 +181,17 @@ __device__ __forceinline__ void chunk_src_b(const StepArgs& a, const PlanB<B>& P
 // ------------------------------------------------------------------ compute waves
 
 // Element offsets (from a.kv) of the cached K rows of round rd's tile that thread (g, sub)
-// holds: rows g + 16 i (i < 4), columns 4 sub .. 4 sub + 3; ~0u for rows at or past the
-// tile's cached rows.  The V rows sit a.kv_v_off further.  (The offsets fit 32 bits:
-// launch_step_batch checks kStepBatchMax * kv_slot_stride.)
+// holds in slots i0 .. i0 + 3: rows g + 16 i, columns 4 sub .. 4 sub + 3; ~0u for rows at or
+// past the tile's cached rows.  The V rows sit a.kv_v_off further.  (The offsets fit 32
+// bits: launch_step_batch checks kStepBatchMax * kv_slot_stride.)
 template <int B>
-__device__ __forceinline__ void tile_rows(const StepArgs& a, const PlanB<B>& P, int rd, size_t kvl, int g, int sub, uint32_t (&off)[4]) {
+__device__ __forceinline__ void tile_rows(const StepArgs& a, const PlanB<B>& P, int rd, int i0, size_t kvl, int g, int sub,
+                                          uint32_t (&off)[4]) {
     int sq = 0, h = 0, s = 0, t0 = 0, R = 0;
     const bool act = P.tile(rd, sq, h, s, t0, R);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int r = g + 16 * i;
+        const int r = g + 16 * (i0 + i);
         off[i] = ~0u;
         if (act && r < R) {
             const int row = t0 + r;
@@ -477,10 +478,13 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
             // c_attn reads, so it may be written while other waves still run c_attn.
             float* qwin = sm.qwin;
             // One tile's rows in registers: the next tile round's K is issued once this tile
-            // round's scores are formed, its V once its weighted sum is.
+            // round's scores are formed, its V once its weighted sum is.  A tile of more than
+            // 64 rows (caches past 768 rows) has the 8 arithmetic slots of attention_kernel:
+            // slots 4-7 are loaded into the same registers once slots 0-3 are used, K for the
+            // scores, then V for the weighted sum, which keeps attention_kernel's order.
             uint32_t off[4];
             float4 kk[4], vv[4];
-            tile_rows<B>(a, P, 0, kvl, g, sub, off);
+            tile_rows<B>(a, P, 0, 0, kvl, g, sub, off);
             load_rows(a.kv, off, kk);
             load_rows(a.kv + a.kv_v_off, off, vv);
             for (int rd = 0; rd < P.rounds; ++rd) {
@@ -513,10 +517,11 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
                 const int nq = act ? pick(P.n, sq) : 0;
                 const int p1 = act ? min(pick(P.L, sq), t0 + pick(P.chunk_rows, sq)) : 0;
                 const int dn = nq - t0 - g;
-                const int i_new = (act && nq < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < 4) ? (dn >> 4) : -1;
+                const int i_new = (act && nq < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < 8) ? (dn >> 4) : -1;
+                const bool wide = act && p1 - t0 > 64;  // the tile has rows in slots 4-7 (uniform)
                 const float* qr = qwin + (rd % kQWin) * kQRec;
                 const float4 q4 = *reinterpret_cast<const float4*>(qr + sub * 4);
-                if (i_new >= 0) {
+                if (i_new >= 0 && i_new < 4) {
                     const float4 kn = *reinterpret_cast<const float4*>(qr + kHeadDim + sub * 4);
                     const float4 vn = *reinterpret_cast<const float4*>(qr + 2 * kHeadDim + sub * 4);
 #pragma unroll
@@ -527,22 +532,40 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
                         }
                     }
                 }
-                float sc[4];
+                float sc[8];
                 float mloc = -INFINITY;
+                auto scores = [&](int i0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float d = q4.x * kk[i].x;
-                    d = __builtin_fmaf(q4.y, kk[i].y, d);
-                    d = __builtin_fmaf(q4.z, kk[i].z, d);
-                    d = __builtin_fmaf(q4.w, kk[i].w, d);
-                    d = sum16_up(d);
-                    const bool valid = act && t0 + g + 16 * i < p1;
-                    sc[i] = valid ? d * 0.125f : -INFINITY;
-                    mloc = fmaxf(mloc, sc[i]);
+                    for (int i = 0; i < 4; ++i) {
+                        float d = q4.x * kk[i].x;
+                        d = __builtin_fmaf(q4.y, kk[i].y, d);
+                        d = __builtin_fmaf(q4.z, kk[i].z, d);
+                        d = __builtin_fmaf(q4.w, kk[i].w, d);
+                        d = sum16_up(d);
+                        const bool valid = act && t0 + g + 16 * (i0 + i) < p1;
+                        sc[i0 + i] = valid ? d * 0.125f : -INFINITY;
+                        mloc = fmaxf(mloc, sc[i0 + i]);
+                    }
+                };
+                scores(0);
+                uint32_t offw[4];
+                if (wide) {
+                    tile_rows<B>(a, P, rd, 4, kvl, g, sub, offw);
+                    load_rows(a.kv, offw, kk);
+                    if (i_new >= 4) {
+                        const float4 kn = *reinterpret_cast<const float4*>(qr + kHeadDim + sub * 4);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (4 + i == i_new) kk[i] = kn;
+                    }
+                    scores(4);
+                } else {
+#pragma unroll
+                    for (int i = 4; i < 8; ++i) sc[i] = -INFINITY;
                 }
                 const bool more = rd + 1 < P.rounds;
                 if (more) {
-                    tile_rows<B>(a, P, rd + 1, kvl, g, sub, off);
+                    tile_rows<B>(a, P, rd + 1, 0, kvl, g, sub, off);
                     load_rows(a.kv, off, kk);
                 }
                 const float wm = wave_max(mloc);
@@ -551,15 +574,28 @@ __global__ __launch_bounds__(kST) void step_batch_kernel(StepArgs a) {
                 const float M = fmaxf(fmaxf(sm.redm[0], sm.redm[1]), fmaxf(sm.redm[2], sm.redm[3]));
                 float lsum = 0.0f;
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                auto weigh = [&](int i0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool valid = act && t0 + g + 16 * i < p1;
-                    const float e = valid ? expf(sc[i] - M) : 0.0f;
-                    lsum += e;
-                    acc.x = __builtin_fmaf(e, vv[i].x, acc.x);
-                    acc.y = __builtin_fmaf(e, vv[i].y, acc.y);
-                    acc.z = __builtin_fmaf(e, vv[i].z, acc.z);
-                    acc.w = __builtin_fmaf(e, vv[i].w, acc.w);
+                    for (int i = 0; i < 4; ++i) {
+                        const bool valid = act && t0 + g + 16 * (i0 + i) < p1;
+                        const float e = valid ? expf(sc[i0 + i] - M) : 0.0f;
+                        lsum += e;
+                        acc.x = __builtin_fmaf(e, vv[i].x, acc.x);
+                        acc.y = __builtin_fmaf(e, vv[i].y, acc.y);
+                        acc.z = __builtin_fmaf(e, vv[i].z, acc.z);
+                        acc.w = __builtin_fmaf(e, vv[i].w, acc.w);
+                    }
+                };
+                weigh(0);
+                if (wide) {
+                    load_rows(a.kv + a.kv_v_off, offw, vv);
+                    if (i_new >= 4) {
+                        const float4 vn = *reinterpret_cast<const float4*>(qr + 2 * kHeadDim + sub * 4);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (4 + i == i_new) vv[i] = vn;
+                    }
+                    weigh(4);
                 }
                 if (more) load_rows(a.kv + a.kv_v_off, off, vv);
                 const float ws = wave_sum(sub == 0 ? lsum : 0.0f);

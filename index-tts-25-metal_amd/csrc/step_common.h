@@ -216,9 +216,7 @@ struct LaneBias {
     }
 };
 
-__device__ __forceinline__ int live_splits_dev(int L, int max_splits) {
-    return min(max_splits, max(1, (L + kAttnSplitRows - 1) / kAttnSplitRows));
-}
+__device__ __forceinline__ int live_splits_dev(int L, int max_splits) { return attn_splits(L, max_splits); }
 
 
 // Wait until chunk c is in a ring of RING chunks (need[] unchanged).

@@ -408,7 +408,8 @@ def both_paths(itts, small_weights):
 @pytest.mark.parametrize("n_text", [10, 40, 300, -900])
 def test_persistent_step_bitwise_equals_multikernel(both_paths, itts, n_text):
     """Same FMA orders, LayerNorm reduction, attention tiles and merge: logits equal bit for bit
-    (KV lengths spanning 1 to 15 attention splits; -900 = a raw 900-row random prefix)."""
+    (KV lengths spanning 1 to 12 attention splits; -900 = a raw 900-row random prefix, whose
+    12 splits of 76 rows use the attention's eight arithmetic slots)."""
     step, multi = both_paths
     if n_text > 0:
         cond, text = itts.synthetic_prefix_inputs(n_text, seed=n_text)
@@ -548,6 +549,26 @@ def test_persistent_batch_generate_equals_multikernel(batch_paths, itts, nseq):
     assert [(r.codes, r.stopped) for r in a] == [(r.codes, r.stopped) for r in b]
     for q in (0, nseq - 1):
         single = step.generate(prefixes[q], opts[q], 40)
+        assert (single.codes, single.stopped) == (a[q].codes, a[q].stopped)
+
+
+def test_persistent_batch_long_caches_equal_multikernel(batch_paths, itts):
+    """Caches of 780-1014 rows: 12 attention splits of 65-85 rows, so the tiles use the
+    attention's eight arithmetic slots (slots 4-7 loaded once 0-3 are used), three tile
+    rounds for three sequences.  Sampled over every code (top_k 0, top_p 1): the persistent
+    batch step, the multi-kernel path and each sequence's batch-1 generate agree."""
+    step, multi = batch_paths
+    prefixes = [itts.synthetic_normal(rows * 1280, 90 + rows, 0.0, 0.5) for rows in (780, 900, 990)]
+    opts = [itts.GenerationOptions(seed=40 + b, top_k=0, top_p=1.0, temperature=1.0, repetition_penalty=1.0, suppress_stop=True)
+            for b in range(3)]
+    print("persistent batch: long caches", flush=True)
+    a = step.generate_batch(prefixes, opts, 24)
+    assert step.last_timing()["decode_path"] == "step"
+    b = multi.generate_batch(prefixes, opts, 24)
+    assert multi.last_timing()["decode_path"] == "multi"
+    assert [(r.codes, r.stopped) for r in a] == [(r.codes, r.stopped) for r in b]
+    for q in range(3):
+        single = step.generate(prefixes[q], opts[q], 24)
         assert (single.codes, single.stopped) == (a[q].codes, a[q].stopped)
 
 

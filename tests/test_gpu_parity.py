@@ -425,6 +425,37 @@ def test_persistent_step_bitwise_equals_multikernel(both_paths, itts, n_text):
         assert np.array_equal(a, b), f"step {i}: max diff {np.max(np.abs(a - b))}"
 
 
+def test_persistent_step_past_2048_rows_bitwise_equals_multikernel(itts, small_weights):
+    """Caches past 2048 rows take 17 or more attention splits of up to 128 rows, so the split
+    merge gathers its records through LDS (one step kernel path, one merge kernel path): a
+    raw 1000-row prefix then 1100 steps to a 2101-row cache, logits equal bit for bit at
+    every step."""
+    import os
+
+    old = os.environ.get("ITTS_GPT_PERSISTENT")
+    try:
+        os.environ["ITTS_GPT_PERSISTENT"] = "0"
+        multi = itts.GptDecoder(small_weights, kv_capacity=4096)
+        os.environ["ITTS_GPT_PERSISTENT"] = "1"
+        step = itts.GptDecoder(small_weights, kv_capacity=4096)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT"] = old
+    prefix = itts.synthetic_normal(1000 * 1280, 55, 0.0, 0.5)
+    assert np.array_equal(step.prefill(prefix), multi.prefill(prefix))
+    codes = np.random.default_rng(3).integers(0, 8192, 1100)
+    for i, code in enumerate(codes):
+        a = step.step(int(code), 2 + i % 1800)
+        b = multi.step(int(code), 2 + i % 1800)
+        assert np.array_equal(a, b), f"step {i} ({1000 + i} cached rows): max diff {np.max(np.abs(a - b))}"
+    assert step.last_timing()["decode_path"] == "step" and multi.last_timing()["decode_path"] == "multi"
+    assert step.cached_tokens() == multi.cached_tokens() == 2100
+    step.close()
+    multi.close()
+
+
 def test_persistent_generate_equals_multikernel(both_paths, itts):
     step, multi = both_paths
     cond, text = itts.synthetic_prefix_inputs(60, seed=5)
@@ -570,6 +601,39 @@ def test_persistent_batch_long_caches_equal_multikernel(batch_paths, itts):
     for q in range(3):
         single = step.generate(prefixes[q], opts[q], 24)
         assert (single.codes, single.stopped) == (a[q].codes, a[q].stopped)
+
+
+def test_persistent_batch_past_2048_rows_equals_multikernel(itts, small_weights):
+    """Three sequences from raw 1000-row prefixes to 2100-row caches: past 2048 rows 17
+    attention splits per (sequence, head), merged through LDS.  Sampled over every code:
+    the persistent batch step, the multi-kernel path and the first sequence's batch-1
+    generate agree."""
+    import os
+
+    old = os.environ.get("ITTS_GPT_PERSISTENT_BATCH")
+    try:
+        os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "0"
+        multi = itts.GptDecoder(small_weights, kv_capacity=4096, max_batch=3)
+        os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "1"
+        step = itts.GptDecoder(small_weights, kv_capacity=4096, max_batch=3)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT_BATCH"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT_BATCH"] = old
+    prefixes = [itts.synthetic_normal(1000 * 1280, 60 + b, 0.0, 0.5) for b in range(3)]
+    opts = [itts.GenerationOptions(seed=70 + b, top_k=0, top_p=1.0, temperature=1.0, repetition_penalty=1.0, suppress_stop=True)
+            for b in range(3)]
+    print("persistent batch: caches past 2048 rows", flush=True)
+    a = step.generate_batch(prefixes, opts, 1100)
+    assert step.last_timing()["decode_path"] == "step"
+    b = multi.generate_batch(prefixes, opts, 1100)
+    assert multi.last_timing()["decode_path"] == "multi"
+    assert [(r.codes, r.stopped) for r in a] == [(r.codes, r.stopped) for r in b]
+    single = step.generate(prefixes[0], opts[0], 1100)
+    assert (single.codes, single.stopped) == (a[0].codes, a[0].stopped)
+    step.close()
+    multi.close()
 
 
 @pytest.mark.parametrize("opts", [

@@ -30,6 +30,7 @@ constexpr int NWAVE = NT / 64;
 constexpr int IPT = (V + NT - 1) / NT;  // score entries per thread (9): i = t + q * NT, q < IPT
 constexpr int kSortMax = 16384;          // next power of two >= V
 constexpr int kSmallProbs = 1024;
+static_assert(kSortMax / 2 >= kSmallProbs + 8, "running sums past the keys in the sort buffer");
 constexpr uint16_t kRemoved = 0x8000;
 
 enum Status : uint32_t {
@@ -47,18 +48,20 @@ enum Status : uint32_t {
 template <int NTT>
 struct SmemT {
     static constexpr int kWaves = NTT / 64, kIpt = (V + NTT - 1) / NTT;
-    union {
+    // s[] / the sort keys; with at most kSmallProbs survivors the keys leave the upper half
+    // free for the draw's and the top-p cut's running sums (16-byte aligned double pairs)
+    union alignas(16) {
         float s[V];
         uint64_t sortbuf[kSortMax];
     };
     uint16_t list[V];  // finite survivors in index order; bit 15 = removed by top-p
     uint32_t qoff[kIpt][kWaves];  // compaction: survivors before (q, wave) in index order
     double probs[kSmallProbs];
-    uint32_t hist[256];
+    uint32_t hist[2][256];  // radix counters, one set per pass parity
     uint32_t wtot[kWaves];
     float wmax[kWaves];
     uint32_t widx[kWaves];
-    uint32_t sel[2];
+    uint32_t sel[2][2];     // radix choice (digit, count above it), one per pass parity
     uint32_t m;
     uint32_t token;
     uint32_t status;
@@ -89,24 +92,68 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
     const uint64_t hi = readlane_u32(static_cast<uint32_t>(u >> 32), l);
     return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
 }
-// kk-th largest value (1-based) of s[0..V): MSB-first radix select on order-preserving keys.
+// X[0] + X[1] + ... + X[n8 - 1] in index order (double), by the calling lane, with X in
+// LDS (16-byte aligned, n8 a multiple of 8); with kWrite, X[j] becomes the running sum
+// X[0] + ... + X[j].  Each group of 8 is read while the previous one is added.
+template <bool kWrite>
+__device__ __forceinline__ double running_sum(double* X, uint32_t n8) {
+    double2* x2 = reinterpret_cast<double2*>(X);
+    double t = 0.0;
+    double2 c[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c[k] = x2[k];
+    for (uint32_t j = 0; j < n8; j += 8) {
+        const uint32_t nx = min(j + 8, n8 - 8) >> 1;  // in bounds; unused past the end
+        double2 nn[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) nn[k] = x2[nx + k];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            t += c[k].x;
+            c[k].x = t;
+            t += c[k].y;
+            c[k].y = t;
+            if (kWrite) x2[(j >> 1) + k] = c[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c[k] = nn[k];
+    }
+    return t;
+}
+
+// kk-th largest value (1-based) of s[0..V): MSB-first radix select on order-preserving keys,
+// 8 bits per pass.  Each thread keeps its keys in registers; the counters and the choice are
+// double-buffered by pass parity, so a pass needs two barriers (counts done, choice made):
+// the next pass's counters are cleared while this pass counts (the previous pass's scan,
+// their last reader, finished before this pass began).
 template <int NTT>
 __device__ inline float radix_kth_largest(SmemT<NTT>& sm, uint32_t kk) {
     [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x, lane = t & 63;
+    uint32_t key[IPT];
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+        const int i = t + q * NT;
+        key[q] = i < V ? float_key(sm.s[i]) : 0u;
+    }
+    if (t < 256) sm.hist[0][t] = 0;
+    __syncthreads();
     uint32_t prefix = 0, mask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (t < 256) sm.hist[t] = 0;
-        __syncthreads();
-        for (int i = t; i < V; i += NT) {
-            const uint32_t k = float_key(sm.s[i]);
-            if ((k & mask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 255u], 1u);
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        uint32_t* h = sm.hist[pass & 1];
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V && (key[q] & mask) == prefix) atomicAdd(&h[(key[q] >> shift) & 255u], 1u);
         }
+        if (pass < 3 && t < 256) sm.hist[(pass + 1) & 1][t] = 0;
         __syncthreads();
         if (t < 64) {
             uint32_t c[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) c[q] = sm.hist[255 - 4 * lane - q];
+            for (int q = 0; q < 4; ++q) c[q] = h[255 - 4 * lane - q];
             const uint32_t loc = c[0] + c[1] + c[2] + c[3];
             uint32_t inc = loc;
 #pragma unroll
@@ -130,15 +177,14 @@ __device__ inline float radix_kth_largest(SmemT<NTT>& sm, uint32_t kk) {
                         }
                     }
                 }
-                sm.sel[0] = static_cast<uint32_t>(d);
-                sm.sel[1] = above;
+                sm.sel[pass & 1][0] = static_cast<uint32_t>(d);
+                sm.sel[pass & 1][1] = above;
             }
         }
         __syncthreads();
-        prefix |= sm.sel[0] << shift;
+        prefix |= sm.sel[pass & 1][0] << shift;
         mask |= 0xffu << shift;
-        kk -= sm.sel[1];
-        __syncthreads();
+        kk -= sm.sel[pass & 1][1];
     }
     return key_float(prefix);
 }
@@ -350,9 +396,34 @@ __device__ inline uint32_t run_processors(SmemT<NTT>& sm, const uint8_t* __restr
     }
     __syncthreads();
     bitonic_sort(sm, n);
-    if (t < 64) {
-        // total in index order, then the cumulative mass in ascending (score, index) order:
-        // the divisions P[j] / total run in parallel, the two sums lane-serially.
+    if (t < 64 && m <= static_cast<uint32_t>(kSmallProbs)) {
+        // total in index order, then the cumulative mass in ascending (score, index) order.
+        // Both sums run on lane 0 over values staged in LDS (the sort buffer's upper half:
+        // the keys take at most kSmallProbs entries here); the divisions P[j] / total and the
+        // threshold tests run on all lanes.
+        const int lane = t;
+        double* R = reinterpret_cast<double*>(sm.sortbuf) + kSortMax / 2;
+        const uint32_t m8 = (m + 7u) & ~7u;
+        for (uint32_t j = lane; j < m8; j += 64) R[j] = j < m ? P[j] : 0.0;
+        double total = lane == 0 ? running_sum<false>(R, m8) : 0.0;
+        total = __shfl(total, 0, 64);
+        if (total <= 0.0) {
+            if (lane == 0) sm.status = kZeroMass;
+        } else {
+            if (lane == 0) sm.status = kOk;
+            const double threshold = 1.0 - static_cast<double>(top_p);
+            for (uint32_t q = lane; q < m8; q += 64) R[q] = q < m ? P[static_cast<uint32_t>(sm.sortbuf[q]) >> 1] / total : 0.0;
+            if (lane == 0) (void)running_sum<true>(R, m8);
+            for (uint32_t q = lane; q < m; q += 64)
+                if (R[q] <= threshold) sm.list[static_cast<uint32_t>(sm.sortbuf[q]) >> 1] |= kRemoved;
+            const uint32_t keep = min(m, beams > 1 ? 2u : 1u);
+            if (static_cast<uint32_t>(lane) < keep) {
+                const uint32_t q = m - keep + lane;
+                sm.list[static_cast<uint32_t>(sm.sortbuf[q]) >> 1] &= ~kRemoved;
+            }
+        }
+    } else if (t < 64) {
+        // more survivors (weights in global memory): the same sums, lane-serially
         const int lane = t;
         double total = 0.0;
         for (uint32_t c0 = 0; c0 < m; c0 += 64) {
@@ -451,6 +522,42 @@ __device__ inline uint32_t draw_token_wave(const SmemT<NTT>& sm, uint32_t m, con
     return last_finite;
 }
 
+// draw_token_wave for up to kSmallProbs survivors (weights P in LDS), `draws` times from the
+// same weights: lane 0 forms the running sums of the live weights in index order once, in
+// LDS (the sort buffer's upper half, free once the processors are done); the walk's running
+// value at survivor j is that sum (it adds the same values in the same order, zeros aside),
+// so each draw's pick, the first live survivor with target < its running sum (else the last
+// live one), takes one ballot per 64 survivors.  Writes the tokens through emit(d, token);
+// returns kOk or kZeroMass.
+template <int NTT, class Emit>
+__device__ inline uint32_t draw_tokens_lds(SmemT<NTT>& sm, uint32_t m, const double* P, uint64_t& rng, int draws, Emit emit) {
+    const int lane = threadIdx.x & 63;
+    double* W = reinterpret_cast<double*>(sm.sortbuf) + kSortMax / 2;
+    const uint32_t m8 = (m + 7u) & ~7u;
+    for (uint32_t j = lane; j < m8; j += 64) W[j] = j < m && !(sm.list[j] & kRemoved) ? P[j] : 0.0;
+    double total = lane == 0 ? running_sum<true>(W, m8) : 0.0;
+    total = __shfl(total, 0, 64);
+    if (total <= 0.0) return kZeroMass;
+    for (int d = 0; d < draws; ++d) {
+        const double target = splitmix_unit(rng) * total;
+        uint32_t pick = 0xffffffffu, last = 0xffffffffu;
+        for (uint32_t c0 = 0; c0 < m; c0 += 64) {
+            const uint32_t j = c0 + lane;
+            const bool live = j < m && !(sm.list[j] & kRemoved) && P[j] > 0.0;
+            const uint64_t hit = __ballot(live && target < W[j]);
+            const uint64_t any = __ballot(live);
+            if (hit) {
+                pick = c0 + static_cast<uint32_t>(__builtin_ctzll(hit));
+                break;
+            }
+            if (any) last = c0 + 63u - static_cast<uint32_t>(__builtin_clzll(any));
+        }
+        if (pick == 0xffffffffu) pick = last;
+        emit(d, static_cast<uint32_t>(sm.list[pick] & 0x7fff));
+    }
+    return kOk;
+}
+
 // One sequence's sampler pass (the body of sampler_kernel, and the fused tail of the persistent
 // step kernel): the processors and the draw on row b of the logits, then, in decode mode, the
 // token accepted and the state advanced (gpt_sampling.cpp:168-189 per step).  Every thread of
@@ -526,9 +633,16 @@ __device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b)
                 const double* P = m <= static_cast<uint32_t>(kSmallProbs) ? sm.probs : Pg;
                 uint64_t rng = st.rng;
                 const int draws = a.mode == kModeDraw ? a.draws : 1;
-                for (int d = 0; d < draws && status == kOk; ++d) {
-                    token = draw_token_wave(sm, m, P, rng, &status);
-                    if (a.mode == kModeDraw && t == 0) a.out_tokens[d] = token;
+                if (m <= static_cast<uint32_t>(kSmallProbs)) {
+                    status = draw_tokens_lds(sm, m, P, rng, draws, [&](int d, uint32_t tk) {
+                        token = tk;
+                        if (a.mode == kModeDraw && t == 0) a.out_tokens[d] = tk;
+                    });
+                } else {
+                    for (int d = 0; d < draws && status == kOk; ++d) {
+                        token = draw_token_wave(sm, m, P, rng, &status);
+                        if (a.mode == kModeDraw && t == 0) a.out_tokens[d] = token;
+                    }
                 }
                 if (t == 0) st.rng = rng;
             }

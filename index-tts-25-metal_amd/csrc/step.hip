@@ -551,19 +551,16 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 const int kc = act ? Plan::kv_chunks(R) : 0;
                 // 8 arithmetic slots as attention_kernel (rows g + 16 i of a tile of up to
                 // kAttnMaxChunk rows); slots past the tile's rows are zeros with -inf scores,
-                // exactly as in the multi-kernel path.
+                // exactly as in the multi-kernel path.  Slots 4-7 hold rows only in tiles of
+                // more than 64 rows (caches past 768 rows; wide, uniform): other tiles run the
+                // code with four slots, where those slots' -inf scores and zero weights, which
+                // leave every sum unchanged, are dropped at compile time.
                 constexpr int PER = kAttnMaxChunk / 16;
-                constexpr int PERL = PER;
-                float4 k4[PER], v4[PER];
-#pragma unroll
-                for (int i = 0; i < PER; ++i) {
-                    k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    v4[i] = k4[i];
-                }
+                const bool wide = act && p1 - t0 > 64;
+                const int dn = static_cast<int>(n) - t0 - g;
+                const int i_new = (act && static_cast<int>(n) < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < PER) ? (dn >> 4) : -1;
                 // q and, in the tile holding it, the row appended by this step (row n): loads in
                 // flight while the cached rows move from the ring to registers
-                const int dn = static_cast<int>(n) - t0 - g;
-                const int i_new = (act && static_cast<int>(n) < p1 && dn >= 0 && (dn & 15) == 0 && (dn >> 4) < PERL) ? (dn >> 4) : -1;
                 int idx[12];
                 bool use[12];
 #pragma unroll
@@ -576,67 +573,80 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 }
                 XRead<12> xr;
                 xr.issue(XB, idx, use, eq);
-                // cached rows from the ring; need stays at the tile's first chunk until its rows
-                // are in registers
-                for (int j = 0; j < 2 * kc; ++j) (void)wait_chunk<kRing>(ctl, ring, ca + j, a.err, failed);
+                float M = 0.0f, lsum = 0.0f;
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                auto tile_math = [&](auto slots) {
+                    constexpr int PERL = decltype(slots)::value;
+                    float4 k4[PERL], v4[PERL];
 #pragma unroll
-                for (int i = 0; i < PERL; ++i) {
-                    const int r = g + 16 * i;  // tile-local row
-                    if (act && r < R) {
-                        const float* kch = ring + ((ca + r / kKvRowsPerChunk) % kRing) * kChunkF;
-                        const float* vch = ring + ((ca + kc + r / kKvRowsPerChunk) % kRing) * kChunkF;
-                        const int off = (r % kKvRowsPerChunk) * kHeadDim + sub * 4;
-                        k4[i] = *reinterpret_cast<const float4*>(kch + off);
-                        v4[i] = *reinterpret_cast<const float4*>(vch + off);
+                    for (int i = 0; i < PERL; ++i) {
+                        k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                        v4[i] = k4[i];
                     }
-                }
-                ca += 2 * kc;
-                release_to(ctl, ca, wave);  // this tile's chunks are in registers now
-                float4 q4;
-                {
-                    float qv[12];
-                    xr.wait(XB, idx, eq, qv, a.err, failed);
-                    q4 = make_float4(qv[0], qv[1], qv[2], qv[3]);
-                    const float4 kn = make_float4(qv[4], qv[5], qv[6], qv[7]);
-                    const float4 vn = make_float4(qv[8], qv[9], qv[10], qv[11]);
+                    // cached rows from the ring; need stays at the tile's first chunk until its
+                    // rows are in registers
+                    for (int j = 0; j < 2 * kc; ++j) (void)wait_chunk<kRing>(ctl, ring, ca + j, a.err, failed);
 #pragma unroll
-                    for (int i = 0; i < PER; ++i) {
-                        if (i == i_new) {
-                            k4[i] = kn;
-                            v4[i] = vn;
+                    for (int i = 0; i < PERL; ++i) {
+                        const int r = g + 16 * i;  // tile-local row
+                        if (act && r < R) {
+                            const float* kch = ring + ((ca + r / kKvRowsPerChunk) % kRing) * kChunkF;
+                            const float* vch = ring + ((ca + kc + r / kKvRowsPerChunk) % kRing) * kChunkF;
+                            const int off = (r % kKvRowsPerChunk) * kHeadDim + sub * 4;
+                            k4[i] = *reinterpret_cast<const float4*>(kch + off);
+                            v4[i] = *reinterpret_cast<const float4*>(vch + off);
                         }
                     }
-                }
-                // scores, max-subtracted exp, partial sums: attention_kernel (decode.hip) op for op
-                float sc[PER];
-                float mloc = -INFINITY;
+                    ca += 2 * kc;
+                    release_to(ctl, ca, wave);  // this tile's chunks are in registers now
+                    float4 q4;
+                    {
+                        float qv[12];
+                        xr.wait(XB, idx, eq, qv, a.err, failed);
+                        q4 = make_float4(qv[0], qv[1], qv[2], qv[3]);
+                        const float4 kn = make_float4(qv[4], qv[5], qv[6], qv[7]);
+                        const float4 vn = make_float4(qv[8], qv[9], qv[10], qv[11]);
 #pragma unroll
-                for (int i = 0; i < PER; ++i) {
-                    float d = q4.x * k4[i].x;
-                    d = __builtin_fmaf(q4.y, k4[i].y, d);
-                    d = __builtin_fmaf(q4.z, k4[i].z, d);
-                    d = __builtin_fmaf(q4.w, k4[i].w, d);
-                    d = sum16_up(d);
-                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
-                    sc[i] = valid ? d * 0.125f : -INFINITY;
-                    mloc = fmaxf(mloc, sc[i]);
-                }
-                const float wm = wave_max(mloc);
-                if (lane == 0) sm.redm[wave] = wm;
-                cbar(ctl, gen, a.err, failed);
-                const float M = fmaxf(fmaxf(sm.redm[0], sm.redm[1]), fmaxf(sm.redm[2], sm.redm[3]));
-                float lsum = 0.0f;
-                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                        for (int i = 0; i < PERL; ++i) {
+                            if (i == i_new) {
+                                k4[i] = kn;
+                                v4[i] = vn;
+                            }
+                        }
+                    }
+                    // scores, max-subtracted exp, partial sums: attention_kernel (decode.hip) op for op
+                    float sc[PERL];
+                    float mloc = -INFINITY;
 #pragma unroll
-                for (int i = 0; i < PER; ++i) {
-                    const bool valid = i < PERL && act && t0 + g + 16 * i < p1;
-                    const float e = valid ? expf(sc[i] - M) : 0.0f;
-                    lsum += e;
-                    acc.x = __builtin_fmaf(e, v4[i].x, acc.x);
-                    acc.y = __builtin_fmaf(e, v4[i].y, acc.y);
-                    acc.z = __builtin_fmaf(e, v4[i].z, acc.z);
-                    acc.w = __builtin_fmaf(e, v4[i].w, acc.w);
-                }
+                    for (int i = 0; i < PERL; ++i) {
+                        float d = q4.x * k4[i].x;
+                        d = __builtin_fmaf(q4.y, k4[i].y, d);
+                        d = __builtin_fmaf(q4.z, k4[i].z, d);
+                        d = __builtin_fmaf(q4.w, k4[i].w, d);
+                        d = sum16_up(d);
+                        const bool valid = act && t0 + g + 16 * i < p1;
+                        sc[i] = valid ? d * 0.125f : -INFINITY;
+                        mloc = fmaxf(mloc, sc[i]);
+                    }
+                    const float wm = wave_max(mloc);
+                    if (lane == 0) sm.redm[wave] = wm;
+                    cbar(ctl, gen, a.err, failed);
+                    M = fmaxf(fmaxf(sm.redm[0], sm.redm[1]), fmaxf(sm.redm[2], sm.redm[3]));
+#pragma unroll
+                    for (int i = 0; i < PERL; ++i) {
+                        const bool valid = act && t0 + g + 16 * i < p1;
+                        const float e = valid ? expf(sc[i] - M) : 0.0f;
+                        lsum += e;
+                        acc.x = __builtin_fmaf(e, v4[i].x, acc.x);
+                        acc.y = __builtin_fmaf(e, v4[i].y, acc.y);
+                        acc.z = __builtin_fmaf(e, v4[i].z, acc.z);
+                        acc.w = __builtin_fmaf(e, v4[i].w, acc.w);
+                    }
+                };
+                if (wide)
+                    tile_math(std::integral_constant<int, PER>{});
+                else
+                    tile_math(std::integral_constant<int, PER / 2>{});
                 const float ws = wave_sum(sub == 0 ? lsum : 0.0f);
                 if (lane == 0) sm.reds[wave] = ws;
                 sm.accs[g][sub * 4 + 0] = acc.x;

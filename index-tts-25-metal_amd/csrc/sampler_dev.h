@@ -121,26 +121,78 @@ __device__ __forceinline__ double running_sum(double* X, uint32_t n8) {
     return t;
 }
 
+// Maximum of v over the wave (the xor butterfly of common.h's wave reductions, on integers).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = max(p[0], p[1]);
+    }
+    {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = max(p[0], p[1]);
+    }
+    int x = static_cast<int>(v);
+    x = static_cast<int>(max(static_cast<uint32_t>(x), static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false))));
+    {
+        int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);  // banks 0, 2: lane + 4
+        t = __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);      // banks 1, 3: lane - 4
+        x = static_cast<int>(max(static_cast<uint32_t>(x), static_cast<uint32_t>(t)));
+    }
+    x = static_cast<int>(max(static_cast<uint32_t>(x), static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false))));
+    x = static_cast<int>(max(static_cast<uint32_t>(x), static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false))));
+    return static_cast<uint32_t>(x);
+}
+
 // kk-th largest value (1-based) of s[0..V): MSB-first radix select on order-preserving keys,
 // 8 bits per pass.  Each thread keeps its keys in registers; the counters and the choice are
 // double-buffered by pass parity, so a pass needs two barriers (counts done, choice made):
 // the next pass's counters are cleared while this pass counts (the previous pass's scan,
 // their last reader, finished before this pass began).
+// The first digit (sign and exponent bits) falls in a few bins, where the per-lane counter
+// atomics collide.  So the keys' maximum comes first: when at least kk keys share its first
+// digit, that digit is the answer's (no key lies in a higher bin) and the first pass is
+// skipped; otherwise it runs as the others.
 template <int NTT>
 __device__ inline float radix_kth_largest(SmemT<NTT>& sm, uint32_t kk) {
     [[maybe_unused]] constexpr int NT = NTT, NWAVE = NTT / 64, IPT = (V + NTT - 1) / NTT;
-    const int t = threadIdx.x, lane = t & 63;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     uint32_t key[IPT];
+    uint32_t kmax = 0;
 #pragma unroll
     for (int q = 0; q < IPT; ++q) {
         const int i = t + q * NT;
         key[q] = i < V ? float_key(sm.s[i]) : 0u;
+        kmax = max(kmax, key[q]);  // padding keys are 0, below every real key but -NaN's
     }
-    if (t < 256) sm.hist[0][t] = 0;
+    kmax = wave_max_u32(kmax);
+    if (lane == 0) sm.qoff[0][wave] = kmax;
+    if (t < 256) {
+        sm.hist[0][t] = 0;
+        sm.hist[1][t] = 0;
+    }
     __syncthreads();
-    uint32_t prefix = 0, mask = 0;
+    kmax = sm.qoff[0][0];
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
+    for (int w = 1; w < NWAVE; ++w) kmax = max(kmax, sm.qoff[0][w]);
+    const uint32_t top = kmax >> 24;
+    uint32_t c = 0;
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+        const int i = t + q * NT;
+        c += static_cast<uint32_t>(__popcll(__ballot(i < V && (key[q] >> 24) == top)));
+    }
+    if (lane == 0) sm.wtot[wave] = c;
+    __syncthreads();
+    uint32_t same = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) same += sm.wtot[w];
+    uint32_t prefix = 0, mask = 0;
+    const int first = same >= kk ? 1 : 0;
+    if (first) {
+        prefix = top << 24;
+        mask = 0xffu << 24;
+    }
+    for (int pass = first; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
         uint32_t* h = sm.hist[pass & 1];
 #pragma unroll
@@ -151,10 +203,10 @@ __device__ inline float radix_kth_largest(SmemT<NTT>& sm, uint32_t kk) {
         if (pass < 3 && t < 256) sm.hist[(pass + 1) & 1][t] = 0;
         __syncthreads();
         if (t < 64) {
-            uint32_t c[4];
+            uint32_t cc[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) c[q] = h[255 - 4 * lane - q];
-            const uint32_t loc = c[0] + c[1] + c[2] + c[3];
+            for (int q = 0; q < 4; ++q) cc[q] = h[255 - 4 * lane - q];
+            const uint32_t loc = cc[0] + cc[1] + cc[2] + cc[3];
             uint32_t inc = loc;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -169,11 +221,11 @@ __device__ inline float radix_kth_largest(SmemT<NTT>& sm, uint32_t kk) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     if (d < 0) {
-                        if (run + c[q] >= kk) {
+                        if (run + cc[q] >= kk) {
                             d = 255 - 4 * lane - q;
                             above = run;
                         } else {
-                            run += c[q];
+                            run += cc[q];
                         }
                     }
                 }

@@ -15,14 +15,17 @@
 // batch-1 order and reduced with the batch-1 pairings), so every sequence's logits are
 // bitwise those of a batch-1 step.
 //
-// LDS: the phase inputs of all B sequences share one staging area (B x 5120 floats), so
-// the ring is smaller than step.hip's (22, 18, 14 chunks for B = 2, 3, 4) and row groups
-// span at most ring - 1 chunks.  Rows go in groups of four and 5120-wide rows one at a time
-// (step.hip's five-row groups and row pairs need more registers than B inputs leave).  A GEMV's input rows stay in LDS (a LayerNorm phase writes the
-// normalised row next to the raw one) and are read 16 bytes per lane per piece, so the
-// registers hold only the row group's weights and B accumulators.  Since consecutive phases
-// reuse the staging area, each phase ends its reads of it at a compute-wave barrier before
-// the next phase writes.
+// LDS: the phase inputs of all B sequences share one staging area of 2560 floats per
+// sequence, and the ring takes the rest (26, 24, 22 chunks for B = 2, 3, 4), enough to hold
+// a workgroup's 20 mlp.c_fc chunks, or its 20 mlp.c_proj chunks, at once.  mlp.c_proj's
+// 5120-wide rows run in two halves (first two chunks of every row against activations
+// 0-2559, then the last two), the accumulators carried across.  Rows go in groups of four,
+// a wave's last five in one group; 5120-wide rows one at a time (step.hip's row pairs need
+// more registers than B inputs leave).  A GEMV's input rows stay in LDS (a LayerNorm phase
+// writes the normalised row next to the raw one) and are read 16 bytes per lane per piece,
+// so the registers hold only the row group's weights and B accumulators.  Since
+// consecutive phases reuse the staging area, each phase ends its reads of it at a
+// compute-wave barrier before the next phase writes.
 //
 // Attention differs from step.hip in where the cached K/V rows come from: the compute threads
 // load their tile rows straight into registers, two rounds ahead, instead of the loaders

@@ -28,7 +28,7 @@
 namespace itts {
 namespace {
 
-constexpr int kNW = 4;  // waves per GEMV workgroup
+constexpr int kNW = 4;  // waves per GEMV workgroup with a LayerNorm prologue (ln_block's layout)
 
 // Splits actually used for L keys (attn_splits).
 __device__ __forceinline__ int live_splits(int L, int max_splits) { return attn_splits(L, max_splits); }
@@ -62,16 +62,22 @@ __global__ __launch_bounds__(256) void ln_seq_kernel(GemvArgs a) {
     for (int i = 0; i < 5; ++i) a.xn[b * kWidth + tid + 256 * i] = v[0][i];
 }
 
-template <int COLS, int RPW, int B, typename WT, int PRO, int EPI>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+// NW waves per workgroup: 4 with a LayerNorm prologue or no input staging; a staged batched
+// launch may take 5, so 1280 or 5120 rows make exactly 256 or 512 workgroups and no CU runs
+// a workgroup more than the others.
+template <int COLS, int RPW, int B, typename WT, int PRO, int EPI, int NW = kNW>
+__global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     constexpr int J = COLS / 256;  // 16-byte chunks per lane per row
     constexpr int PER = kWidth / 256;
     static_assert(PRO == kProNone || PRO == kProStaged || COLS == kWidth, "LayerNorm prologue is 1280 wide");
     constexpr bool STAGED = PRO == kProStaged;
+    static_assert(NW == kNW || STAGED, "only a staged GEMV takes another wave count");
+    constexpr int TPB = 64 * NW;
+    static_assert(kWidth % TPB == 0, "thread count divides the 1280-column chunk");
     using LD = WLoad<WT>;
     using VT = typename LD::vec;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = (blockIdx.x * kNW + wave) * RPW;
+    const int row0 = (blockIdx.x * NW + wave) * RPW;
 
     bool any = false;
     for (int b = 0; b < a.nseq; ++b) any |= a.state[b].active != 0;
@@ -101,16 +107,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     // order, so a later request would wait for the whole weight fetch).  16-byte pieces: piece
     // f < B * 320 is columns 4 (f % 320) .. of sequence f / 320.
     // (5120-wide rows, whose four chunks would otherwise hold too many registers at once: 4-byte
-    // pieces, thread t taking columns t + 256 i of each sequence)
+    // pieces, thread t taking columns t + TPB i of each sequence.  Holding a second chunk in
+    // registers spilled at 8 sequences and measured slower.)
     constexpr bool WIDE = COLS > kWidth;
+    constexpr int NCH = COLS / kWidth;             // 1280-column chunks per row
+    constexpr int PX = kWidth / TPB;               // columns per thread, sequence and chunk (wide rows)
     constexpr int XF = kWidth / 4;                  // 16-byte pieces per sequence and chunk
-    constexpr int NX = WIDE ? B * PER : (B * XF + 255) / 256;  // pieces per thread
+    constexpr int NX = WIDE ? B * PX : (B * XF + TPB - 1) / TPB;  // pieces per thread
     using XP = typename std::conditional<WIDE, float, float4>::type;
     XP xr[STAGED ? NX : 1];
-    auto x_piece = [&](int q, int i) -> XP {       // piece tid + 256 i of chunk q
-        const int f = tid + 256 * i;
-        if constexpr (WIDE) {  // i = b * PER + k: column tid + 256 k of sequence b
-            return a.x[(i / PER) * a.x_stride + q * kWidth + tid + 256 * (i % PER)];
+    auto x_piece = [&](int q, int i) -> XP {       // piece tid + TPB i of chunk q
+        const int f = tid + TPB * i;
+        if constexpr (WIDE) {  // i = b * PX + k: column tid + TPB k of sequence b
+            return a.x[(i / PX) * a.x_stride + q * kWidth + tid + TPB * (i % PX)];
         } else {
             return f < B * XF ? *reinterpret_cast<const float4*>(a.x + (f / XF) * a.x_stride + q * kWidth + (f % XF) * 4)
                               : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -160,16 +169,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         // x through LDS, 1280 columns at a time (two buffers when there are several chunks):
         // chunk q + 1 is loaded into registers while chunk q's FMAs run.  Per (row, sequence)
         // the FMA chain runs over j in order, as below.
-        constexpr int NCH = COLS / kWidth;
 #pragma unroll
         for (int q = 0; q < NCH; ++q) {
             float* xq = xs + (q & 1) * B * kWidth;
 #pragma unroll
             for (int i = 0; i < NX; ++i) {
-                const int f = tid + 256 * i;
+                const int f = tid + TPB * i;
                 if (WIDE || f < B * XF) {
                     if constexpr (WIDE) {
-                        xq[(i / PER) * kWidth + tid + 256 * (i % PER)] = xr[i];
+                        xq[(i / PX) * kWidth + tid + TPB * (i % PX)] = xr[i];
                     } else {
                         *reinterpret_cast<float4*>(xq + (f / XF) * kWidth + (f % XF) * 4) = xr[i];
                     }
@@ -262,26 +270,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
 }
 
-template <int COLS, int RPW, int PRO, int EPI, int B>
+template <int COLS, int RPW, int PRO, int EPI, int B, int NW>
 hipError_t launch_b(const GemvArgs& a, bool bf16, hipStream_t s) {
-    const int rows_per_wg = kNW * RPW;
+    const int rows_per_wg = NW * RPW;
     const dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
     if (bf16)
-        hipLaunchKernelGGL((gemv_kernel<COLS, RPW, B, uint16_t, PRO, EPI>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gemv_kernel<COLS, RPW, B, uint16_t, PRO, EPI, NW>), grid, dim3(64 * NW), 0, s, a);
     else
-        hipLaunchKernelGGL((gemv_kernel<COLS, RPW, B, float, PRO, EPI>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gemv_kernel<COLS, RPW, B, float, PRO, EPI, NW>), grid, dim3(64 * NW), 0, s, a);
     return hipGetLastError();
 }
 
-template <int COLS, int RPW, int PRO, int EPI>
+template <int COLS, int RPW, int PRO, int EPI, int NW = kNW>
 hipError_t launch_gemv(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
     switch (gemv_batch_bucket(batch)) {
-        case 1: return launch_b<COLS, RPW, PRO, EPI, 1>(a, bf16, s);
-        case 2: return launch_b<COLS, RPW, PRO, EPI, 2>(a, bf16, s);
-        case 3: return launch_b<COLS, RPW, PRO, EPI, 3>(a, bf16, s);
-        case 4: return launch_b<COLS, RPW, PRO, EPI, 4>(a, bf16, s);
-        case 8: return launch_b<COLS, RPW, PRO, EPI, 8>(a, bf16, s);
-        case 10: return launch_b<COLS, RPW, PRO, EPI, 10>(a, bf16, s);
+        case 1: return launch_b<COLS, RPW, PRO, EPI, 1, kNW>(a, bf16, s);
+        case 2: return launch_b<COLS, RPW, PRO, EPI, 2, NW>(a, bf16, s);
+        case 3: return launch_b<COLS, RPW, PRO, EPI, 3, NW>(a, bf16, s);
+        case 4: return launch_b<COLS, RPW, PRO, EPI, 4, NW>(a, bf16, s);
+        case 8: return launch_b<COLS, RPW, PRO, EPI, 8, NW>(a, bf16, s);
+        case 10: return launch_b<COLS, RPW, PRO, EPI, 10, NW>(a, bf16, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -454,7 +462,9 @@ GemvArgs staged_on_xn(const GemvArgs& a) {
     return b;
 }
 
-// Rows per wave: chosen so every launch has >= 320 workgroups of 4 waves.
+// Rows per wave: chosen so every launch has >= 256 workgroups.  Batched attn.c_proj, mlp.c_fc
+// and mlp.c_proj take workgroups of 5 waves: 256, 512 and 256 of them, an equal share per CU
+// (with 4 waves, 320, 640 and 320: a quarter or half of the CUs ran one more).
 hipError_t launch_gemv_qkv(const GemvArgs& a, int batch, bool bf16, bool embed, hipStream_t s) {
     if (batch >= 2) {
         const hipError_t e = embed ? launch_ln_seq<kProEmbedLn>(a, batch, s) : launch_ln_seq<kProLn>(a, batch, s);
@@ -465,19 +475,19 @@ hipError_t launch_gemv_qkv(const GemvArgs& a, int batch, bool bf16, bool embed, 
                  : launch_gemv<kWidth, 2, kProLn, kEpiQkv>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_proj(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
-    if (batch >= 2) return launch_gemv<kWidth, 1, kProStaged, kEpiResid>(a, batch, bf16, s);
+    if (batch >= 2) return launch_gemv<kWidth, 1, kProStaged, kEpiResid, 5>(a, batch, bf16, s);
     return launch_gemv<kWidth, 1, kProNone, kEpiResid>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_fc(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
     if (batch >= 2) {
         const hipError_t e = launch_ln_seq<kProLn>(a, batch, s);
         if (e != hipSuccess) return e;
-        return launch_gemv<kWidth, 2, kProStaged, kEpiGelu>(staged_on_xn(a), batch, bf16, s);
+        return launch_gemv<kWidth, 2, kProStaged, kEpiGelu, 5>(staged_on_xn(a), batch, bf16, s);
     }
     return launch_gemv<kWidth, 2, kProLn, kEpiGelu>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_fc2(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
-    if (batch >= 2) return launch_gemv<kFfn, 1, kProStaged, kEpiResid>(a, batch, bf16, s);
+    if (batch >= 2) return launch_gemv<kFfn, 1, kProStaged, kEpiResid, 5>(a, batch, bf16, s);
     return launch_gemv<kFfn, 1, kProNone, kEpiResid>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_head(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {

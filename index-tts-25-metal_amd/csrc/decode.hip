@@ -33,11 +33,13 @@ constexpr int kNW = 4;  // waves per GEMV workgroup with a LayerNorm prologue (l
 // Splits actually used for L keys (attn_splits).
 __device__ __forceinline__ int live_splits(int L, int max_splits) { return attn_splits(L, max_splits); }
 
-// The prologue of a batched GEMV, once per sequence: xn[b] = LayerNorm(s) of sequence b's
-// input row (kProEmbedLn: of h = mel_emb[token] + mel_pos[position], also written to h_out).
-// ln_block<1, 5> is the batch-1 prologue's own reduction, so xn[b] holds exactly the values
-// gemv_kernel<.., B = 1, ..> forms in its registers.  (One small launch per LayerNorm measured
-// faster than forming the B LayerNorms in every workgroup of the batched GEMV.)
+// The prologue of a batched GEMV for layer 0's embedding row and the head, once per
+// sequence: xn[b] = LayerNorm(s) of sequence b's input row (kProEmbedLn: of h = mel_emb[token]
+// + mel_pos[position], also written to h_out).  ln_block<1, 5> is the batch-1 prologue's own
+// reduction, so xn[b] holds exactly the values gemv_kernel<.., B = 1, ..> forms in its
+// registers.  The per-layer ln_1 and ln_2 are formed inside the batched GEMV instead
+// (kProStagedLn: from the staged rows in LDS, while the weights are in flight), which saves
+// this launch: 3.3 us per LayerNorm at 8 sequences.
 template <int PRO>
 __global__ __launch_bounds__(256) void ln_seq_kernel(GemvArgs a) {
     const int b = blockIdx.x, tid = threadIdx.x;
@@ -70,7 +72,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     constexpr int J = COLS / 256;  // 16-byte chunks per lane per row
     constexpr int PER = kWidth / 256;
     static_assert(PRO == kProNone || PRO == kProStaged || COLS == kWidth, "LayerNorm prologue is 1280 wide");
-    constexpr bool STAGED = PRO == kProStaged;
+    constexpr bool STAGED = PRO == kProStaged || PRO == kProStagedLn;
     static_assert(NW == kNW || STAGED, "only a staged GEMV takes another wave count");
     constexpr int TPB = 64 * NW;
     static_assert(kWidth % TPB == 0, "thread count divides the 1280-column chunk");
@@ -129,6 +131,17 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < NX; ++i) xr[i] = x_piece(0, i);
     }
+    // kProStagedLn: gamma and beta of the columns t + TPB k this thread normalises, also ahead
+    // of the weights.
+    constexpr int GC = PRO == kProStagedLn ? kWidth / TPB : 1;
+    float gv[GC], bv[GC];
+    if constexpr (PRO == kProStagedLn) {
+#pragma unroll
+        for (int k = 0; k < GC; ++k) {
+            gv[k] = a.ln_w[tid + TPB * k];
+            bv[k] = a.ln_b[tid + TPB * k];
+        }
+    }
 
     const WT* __restrict__ w = static_cast<const WT*>(a.w);
     VT wv[RPW][J];
@@ -184,6 +197,31 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
                 }
             }
             __syncthreads();
+            if constexpr (PRO == kProStagedLn) {
+                // Each sequence's mean and 1 / sqrt(var + eps) by one wave, in ln_block<1, 5>'s
+                // order (ln_stats), then every element normalised in place, as ln_block does:
+                // the rows equal what ln_seq_kernel writes, bit for bit.
+                __shared__ float lnst[B][2];
+                for (int b = wave; b < B; b += NW) {  // wave-uniform: ln_stats needs all 64 lanes
+                    float v[4][5];
+                    ln_layout_load(xq + b * kWidth, lane, v);
+                    float mean, inv;
+                    ln_stats(v, mean, inv);
+                    if (lane == 0) {
+                        lnst[b][0] = mean;
+                        lnst[b][1] = inv;
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+#pragma unroll
+                    for (int k = 0; k < GC; ++k) {
+                        float& e = xq[b * kWidth + tid + TPB * k];
+                        e = ln_apply(e, lnst[b][0], lnst[b][1], gv[k], bv[k]);
+                    }
+                __syncthreads();
+            }
             if (q + 1 < NCH) {
 #pragma unroll
                 for (int i = 0; i < NX; ++i) xr[i] = x_piece(q + 1, i);
@@ -466,8 +504,9 @@ GemvArgs staged_on_xn(const GemvArgs& a) {
 // and mlp.c_proj take workgroups of 5 waves: 256, 512 and 256 of them, an equal share per CU
 // (with 4 waves, 320, 640 and 320: a quarter or half of the CUs ran one more).
 hipError_t launch_gemv_qkv(const GemvArgs& a, int batch, bool bf16, bool embed, hipStream_t s) {
+    if (batch >= 2 && !embed) return launch_gemv<kWidth, 2, kProStagedLn, kEpiQkv>(a, batch, bf16, s);
     if (batch >= 2) {
-        const hipError_t e = embed ? launch_ln_seq<kProEmbedLn>(a, batch, s) : launch_ln_seq<kProLn>(a, batch, s);
+        const hipError_t e = launch_ln_seq<kProEmbedLn>(a, batch, s);
         if (e != hipSuccess) return e;
         return launch_gemv<kWidth, 2, kProStaged, kEpiQkv>(staged_on_xn(a), batch, bf16, s);
     }
@@ -479,11 +518,7 @@ hipError_t launch_gemv_proj(const GemvArgs& a, int batch, bool bf16, hipStream_t
     return launch_gemv<kWidth, 1, kProNone, kEpiResid>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_fc(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
-    if (batch >= 2) {
-        const hipError_t e = launch_ln_seq<kProLn>(a, batch, s);
-        if (e != hipSuccess) return e;
-        return launch_gemv<kWidth, 2, kProStaged, kEpiGelu, 5>(staged_on_xn(a), batch, bf16, s);
-    }
+    if (batch >= 2) return launch_gemv<kWidth, 2, kProStagedLn, kEpiGelu, 5>(a, batch, bf16, s);
     return launch_gemv<kWidth, 2, kProLn, kEpiGelu>(a, batch, bf16, s);
 }
 hipError_t launch_gemv_fc2(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {

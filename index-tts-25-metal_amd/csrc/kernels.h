@@ -13,6 +13,7 @@ enum Prologue : int {
     kProEmbedLn = 2,  // h = mel_emb[token] + mel_pos[position] (written out), x = LayerNorm(h)
     kProLn2 = 3,      // x = LayerNorm_b(LayerNorm_a(x_in)) (ln_f then final_norm)
     kProStaged = 4,   // x read from global as is, through LDS in 1280-column chunks (batches)
+    kProStagedLn = 5, // kProStaged, then x = LayerNorm(x_in) per sequence in LDS (batches)
 };
 enum Epilogue : int {
     kEpiQkv = 0,     // q row / K,V cache append at row n
@@ -47,8 +48,8 @@ struct GemvArgs {
     float* h_out;           // [batch][1280]
     const SeqState* state;  // [batch]
     int nseq;               // sequences with state entries (<= batch template)
-    // batches of 2 or more: the LayerNorm'd input rows [batch][1280], formed once per launch
-    // by a small kernel instead of in every GEMV workgroup
+    // batches of 2 or more, layer 0's embedding row and the head: the LayerNorm'd input rows
+    // [batch][1280], formed once per launch by a small kernel instead of in every GEMV workgroup
     float* xn;
 };
 

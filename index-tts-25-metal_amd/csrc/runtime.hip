@@ -468,11 +468,13 @@ struct Engine {
         HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         HIP_CHECK(step_occupancy(false, &occ));
         if (occ < 1 || !step_fits(cus)) return;
-        // Batches and beams of 2..4 sequences in one launch (step_batch.hip) when this decoder
-        // holds more than one sequence; ITTS_GPT_PERSISTENT_BATCH=0 keeps them on the
-        // multi-kernel path.
+        // Batches and beams of 2..4 sequences in one launch (step_batch.hip) only when
+        // ITTS_GPT_PERSISTENT_BATCH=1: the multi-kernel path's batched GEMVs (five-wave
+        // workgroups, LayerNorms formed in the GEMV) measure as fast at 2 sequences and faster
+        // from 3 on (3: 932 against 1015 us per step, 4: 1036 against 1207; beam-3 3070
+        // against 2824 beam tokens/s), with bitwise the same logits.
         const char* pb = std::getenv("ITTS_GPT_PERSISTENT_BATCH");
-        const bool batch = max_batch >= 2 && !(pb && std::strcmp(pb, "0") == 0);
+        const bool batch = max_batch >= 2 && pb && std::strcmp(pb, "1") == 0;
         for (int nb = 2; batch && nb <= kStepBatchMax; ++nb) {
             int bocc = 0;
             HIP_CHECK(step_batch_occupancy(nb, &bocc));
@@ -537,10 +539,10 @@ struct Engine {
             throw std::runtime_error("GPT decode step: a workgroup hand-off timed out");
         }
     }
-    // The persistent path takes one sequence (step.hip) or 2..kStepBatchMax in one launch
-    // (step_batch.hip; with the beam row-owner table when every slot it may name is below
-    // kStepBatchMax).  Larger batches stay on the multi-kernel path, whose batched GEMVs read
-    // the weights once for all of them (measured faster from 5 sequences on).
+    // The persistent path takes one sequence (step.hip) or, when enabled (init_step),
+    // 2..kStepBatchMax in one launch (step_batch.hip; with the beam row-owner table when every
+    // slot it may name is below kStepBatchMax).  Other batches take the multi-kernel path,
+    // whose batched GEMVs read the weights once for all of them.
     bool persistent(int nseq, bool use_table) const {
         if (!step_ok || nseq < 1 || nseq > kStepBatchMax) return false;
         if (use_table) return nseq >= 2 && step_batch_ok[nseq] && beam_slots <= static_cast<uint32_t>(kStepBatchMax);

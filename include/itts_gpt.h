@@ -231,8 +231,9 @@ int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t c
  * path only. */
 int itts_gpt_step_phases(itts_gpt* h, uint32_t cached_rows, uint32_t iters, float* phase_us);
 /* The same for the persistent batch step kernel with `nseq` (2-4) sequences, each at
- * `cached_rows` cached rows: the forward that batches of 2-4 and beam search run (decoders
- * created with max_batch >= nseq). */
+ * `cached_rows` cached rows: the forward that batches of 2-4 and beam search run when the
+ * decoder was created with max_batch >= nseq and ITTS_GPT_PERSISTENT_BATCH=1 (else the
+ * call fails with an invalid-argument status). */
 int itts_gpt_step_phases_batch(itts_gpt* h, uint32_t nseq, uint32_t cached_rows, uint32_t iters, float* phase_us);
 
 /* ---- EnhancedCodec (src/codec.cpp), the consumer of the semantic codes ----------

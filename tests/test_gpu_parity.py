@@ -505,8 +505,18 @@ def test_two_decoders_concurrently_on_one_gpu(itts, small_weights):
     import dataclasses
     import threading
 
+    import os
+
     a = itts.GptDecoder(small_weights, kv_capacity=1024)
-    b = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=2)
+    old = os.environ.get("ITTS_GPT_PERSISTENT_BATCH")
+    os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "1"  # the batch step is opt-in
+    try:
+        b = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=2)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT_BATCH"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT_BATCH"] = old
     cond, text = itts.synthetic_prefix_inputs(30, seed=12)
     prefix = a.prepare_cond(cond, text, 0)
     o = itts.GenerationOptions(seed=3, suppress_stop=True)

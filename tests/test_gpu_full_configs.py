@@ -4,6 +4,10 @@ The workloads bench.py times, against the CPU oracle:
   * 155-row prefix, 600 sampled codes (KV to 754): codes exact; teacher-forced logits at every
     step against the oracle run live on the host; at every step the device sampler, given the
     device's own logits and the oracle's SplitMix64 state, picks the oracle's code;
+  * 115-row prefix, beam search with 3 beams (length penalty 0, repetition penalty 10), 400
+    codes: sampled beams (seed 7, the bench's beam-3 workload) and greedy beams, codes exact on
+    the default multi-kernel beam path and on the persistent batch step, then teacher-forced
+    logits of the winning hypothesis against the oracle's fixture;
   * 235-row prefix, greedy to 1813 codes (KV to 2047, attention beyond 16 splits): codes exact on
     the persistent step and on the multi-kernel path, whose logits agree bit for bit at every
     step; teacher-forced logits against the oracle's fixture at the stored steps;
@@ -29,7 +33,7 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden" / "full_configs.npz"
 LOGIT_ABS, LOGIT_REL = 1e-3, 1e-4
 REF_ABS, REF_RMSE = 1e-4, 2e-5   # src/main.cpp:47 (compare(name, logits, ref, 1e-4f, 2e-5))
-BF16_ABS = 5e-2                  # BF16-stored weights, FP32 accumulate, against the FP32 oracle
+BF16_ABS = 3e-2                  # BF16-stored weights, FP32 accumulate, against the FP32 oracle (achieved 2.1e-2)
 
 
 class Errors:
@@ -107,6 +111,50 @@ def test_config2_sampled_600(itts, oracle, full_weights, golden):
 def _greedy_divergence(what, got_codes, exp_codes):
     i = next((i for i, (a, b) in enumerate(zip(got_codes, exp_codes)) if a != b), None)
     assert i is None and len(got_codes) == len(exp_codes), f"{what}: codes differ first at {i}"
+
+
+@pytest.mark.parametrize("tag", ["c3s", "c3g"])
+def test_config3_beam3_400(itts, full_weights, golden, tag):
+    """Config 3 at full length (src/gpt_sampling.cpp:190-245; the reference's gpt_test checks beam
+    codes exactly, src/main.cpp:60-63): 3 beams over a 115-row prefix, 400 codes, on the default
+    multi-kernel beam path and on ITTS_GPT_PERSISTENT_BATCH=1, against the oracle's codes; then
+    the winning hypothesis' teacher-forced logits against the oracle's fixture."""
+    codes = [int(c) for c in golden[f"{tag}.codes"]]
+    old = os.environ.get("ITTS_GPT_PERSISTENT_BATCH")
+    try:
+        os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "0"
+        multi = itts.GptDecoder(full_weights, kv_capacity=4096, max_batch=3)
+        os.environ["ITTS_GPT_PERSISTENT_BATCH"] = "1"
+        step = itts.GptDecoder(full_weights, kv_capacity=4096, max_batch=3)
+    finally:
+        if old is None:
+            del os.environ["ITTS_GPT_PERSISTENT_BATCH"]
+        else:
+            os.environ["ITTS_GPT_PERSISTENT_BATCH"] = old
+    cond, text = itts.synthetic_prefix_inputs(80, seed=3)
+    prefix = multi.prepare_cond(cond, text, 0)
+    assert prefix.size // 1280 == 115
+    if tag == "c3s":  # the bench's beam-3 options
+        o = itts.GenerationOptions(num_beams=3, length_penalty=0.0, repetition_penalty=10.0, seed=7, suppress_stop=True)
+    else:
+        o = itts.GenerationOptions(do_sample=False, num_beams=3, length_penalty=0.0, repetition_penalty=10.0,
+                                   suppress_stop=True)
+    for dec, path in ((multi, "multi"), (step, "step")):
+        print(f"config 3 ({tag}): beam-3 generate 400 on the {path} path", flush=True)
+        r = dec.generate(prefix, o, 400)
+        assert dec.last_timing()["decode_path"] == path
+        assert not r.stopped
+        _greedy_divergence(f"config 3 {tag} ({path})", r.codes, codes)
+    print(f"config 3 ({tag}): teacher-forced replay of the winning hypothesis", flush=True)
+    err = Errors(f"config 3 {tag} logits")
+    fixture = dict(zip([int(s) for s in golden[f"{tag}.steps"]], golden[f"{tag}.logits"]))
+    for t in range(max(fixture) + 1):
+        got = multi.prefill(prefix) if t == 0 else multi.step(codes[t - 1], t + 1)
+        if t in fixture:
+            err.add(got, fixture[t], t)
+    err.check()
+    step.close()
+    multi.close()
 
 
 def test_config4_long_context_greedy(itts, full_weights, golden):

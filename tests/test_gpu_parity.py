@@ -456,6 +456,83 @@ def test_persistent_step_past_2048_rows_bitwise_equals_multikernel(itts, small_w
     multi.close()
 
 
+def _step_paths(itts, weights, var, **kw):
+    """Two decoders over the same weights: `var`=0 (multi-kernel path) and `var`=1 (persistent)."""
+    import os
+
+    old = os.environ.get(var)
+    try:
+        os.environ[var] = "0"
+        multi = itts.GptDecoder(weights, kv_capacity=4096, **kw)
+        os.environ[var] = "1"
+        step = itts.GptDecoder(weights, kv_capacity=4096, **kw)
+    finally:
+        if old is None:
+            del os.environ[var]
+        else:
+            os.environ[var] = old
+    return step, multi
+
+
+def test_past_2048_rows_to_the_reference_limit_match_oracle(itts, oracle, small_weights):
+    """The longest cache the reference admits: a 1024-row prefix (src/gpt.cpp:73) and 1813
+    teacher-forced steps at mel positions 2..1814 (src/gpt_sampling.cpp:169), so the last step
+    attends over 2837 rows.  From 2049 rows on, every step takes 17-23 attention splits and the
+    split merge gathers its records through LDS.  Both the persistent step and the multi-kernel
+    path are compared with the CPU oracle (not only with each other) at every step from 2040
+    cached rows on, at the path's bar and at the reference's gpt_test bar (src/main.cpp:47)."""
+    step, multi = _step_paths(itts, small_weights, "ITTS_GPT_PERSISTENT")
+    orc = oracle.OracleGpt(small_weights, kv_capacity=4096)
+    prefix = itts.synthetic_normal(1024 * 1280, 56, 0.0, 0.5)
+    print("past 2048 rows vs oracle: 1024-row prefix, 1813 steps", flush=True)
+    ref = orc.prefill(prefix)
+    assert_logits_close(step.prefill(prefix), ref, "persistent prefill")
+    assert_logits_close(multi.prefill(prefix), ref, "multi-kernel prefill")
+    codes = np.random.default_rng(4).integers(0, 8192, 1813)
+    worst_abs, worst_rmse, compared = 0.0, 0.0, 0
+    for i, code in enumerate(codes):
+        rows = 1024 + i + 1  # cache length after this step
+        ref = orc.step(int(code), i + 2)
+        a = step.step(int(code), i + 2)
+        b = multi.step(int(code), i + 2)
+        if rows < 2040:
+            continue
+        for got, what in ((a, "persistent"), (b, "multi-kernel")):
+            assert_logits_close(got, ref, f"{what} step {i} ({rows} cached rows)")
+            d = np.abs(got.astype(np.float64) - ref)
+            worst_abs, worst_rmse = max(worst_abs, float(d.max())), max(worst_rmse, float(np.sqrt(np.mean(d * d))))
+        compared += 1
+    assert step.last_timing()["decode_path"] == "step" and multi.last_timing()["decode_path"] == "multi"
+    assert step.cached_tokens() == multi.cached_tokens() == orc.cached_tokens() == 2837
+    print(f"{compared} steps at 2040-2837 rows: worst max-abs {worst_abs:.3e}, rmse {worst_rmse:.3e}", flush=True)
+    assert worst_abs < 1e-4 and worst_rmse < 2e-5
+    step.close()
+    multi.close()
+
+
+def test_batch_past_2048_rows_to_the_reference_limit_match_oracle(itts, oracle, small_weights):
+    """Three sequences of 1024-row prefixes, 1813 sampled codes each (caches to 2837 rows, up
+    to 23 attention splits per (sequence, head)): the codes of the persistent batch step and of
+    the multi-kernel batch path both equal the CPU oracle's generate for every sequence."""
+    step, multi = _step_paths(itts, small_weights, "ITTS_GPT_PERSISTENT_BATCH", max_batch=3)
+    orc = oracle.OracleGpt(small_weights, kv_capacity=4096)
+    prefixes = [itts.synthetic_normal(1024 * 1280, 160 + b, 0.0, 0.5) for b in range(3)]
+    opts = [itts.GenerationOptions(seed=170 + b, top_k=0, top_p=1.0, temperature=1.0, repetition_penalty=1.0,
+                                   suppress_stop=True) for b in range(3)]
+    print("batch past 2048 rows vs oracle: 3 x (1024-row prefix, 1813 codes)", flush=True)
+    a = step.generate_batch(prefixes, opts, 1813)
+    assert step.last_timing()["decode_path"] == "step"
+    b = multi.generate_batch(prefixes, opts, 1813)
+    assert multi.last_timing()["decode_path"] == "multi"
+    for q in range(3):
+        exp = orc.generate(prefixes[q], oracle.options_from(opts[q]), 1813)
+        assert len(exp[0]) == 1813
+        assert (a[q].codes, a[q].stopped) == exp, f"persistent batch, sequence {q}"
+        assert (b[q].codes, b[q].stopped) == exp, f"multi-kernel batch, sequence {q}"
+    step.close()
+    multi.close()
+
+
 def test_persistent_generate_equals_multikernel(both_paths, itts):
     step, multi = both_paths
     cond, text = itts.synthetic_prefix_inputs(60, seed=5)

@@ -19,9 +19,14 @@ What pins each one (tests/test_codec_oracle.py): conv kernels that are a unit im
 j shift the input by j - pad (identity at j = pad) and a brute-force loop over the Metal
 kernel's index arithmetic on tiny shapes; LayerNorm rows have zero mean and unit variance;
 the GELU's erf is within the published 1.5e-7 bound of math.erf on a dense grid (a wrong
-coefficient breaks the bound); the upsampling equals np.repeat(x, 2).  vocos() and decode()
-only compose those pieces in codec.cpp's order (36-48, 64-72); no check of their own pins the
-composition beyond its pinned parts (its agreement with the HIP decode is parity, not a pin).
+coefficient breaks the bound); the upsampling equals np.repeat(x, 2).
+The composition (vocos() and decode(), codec.cpp:36-48 and 64-72) is pinned by two checks:
+with every layer scale gamma = 0 the ConvNeXt blocks are the identity and decode() reduces to
+up(repeat2(linear(LN(LN(embed(lookup)))))); and decode() equals an independent float64
+forward built from torch's conv1d / layer_norm / gelu / linear / interpolate in the published
+Vocos backbone's channels-first form.  MUTATION plants one mistake at a time (a dropped
+residual, the x2 upsampling after codec.up, pwconv1 and pwconv2 swapped as transposes, the
+block's LayerNorm before its depthwise conv, the GELU after pwconv2); each must fail a check.
 """
 from __future__ import annotations
 
@@ -32,6 +37,7 @@ import numpy as np
 
 WIDTH, HIDDEN, FFN, BLOCKS, CODEBOOK = 1024, 384, 2048, 12, 8192
 EPS = 1e-6
+MUTATION = None  # tests only: None, or one planted mistake (see the module docstring)
 
 _AS = (0.254829592, -0.284496736, 1.421413741, -1.453152027, 1.061405429)  # Abramowitz & Stegun 7.1.26
 _AS_P = 0.3275911
@@ -108,11 +114,22 @@ def vocos(weights: Dict[str, np.ndarray], x: np.ndarray, prefix: str = "codec.de
                   _w(weights, p + ".norm.weight"), _w(weights, p + ".norm.bias"))
     for i in range(blocks):
         l = f"{p}.convnext.{i}"
-        h = layernorm(dwconv_same(x, _w(weights, l + ".dwconv.weight"), _w(weights, l + ".dwconv.bias")),
-                      _w(weights, l + ".norm.weight"), _w(weights, l + ".norm.bias"))
-        h = codec_gelu(linear(h, _w(weights, l + ".pwconv1.weight"), _w(weights, l + ".pwconv1.bias")))
-        h = linear(h, _w(weights, l + ".pwconv2.weight"), _w(weights, l + ".pwconv2.bias"))
-        x = x + h * _w(weights, l + ".gamma")
+        dw = (_w(weights, l + ".dwconv.weight"), _w(weights, l + ".dwconv.bias"))
+        ln = (_w(weights, l + ".norm.weight"), _w(weights, l + ".norm.bias"))
+        w1, w2 = _w(weights, l + ".pwconv1.weight"), _w(weights, l + ".pwconv2.weight")
+        if MUTATION == "swap_pw":
+            w1, w2 = w2.T, w1.T
+        if MUTATION == "norm_first":
+            h = dwconv_same(layernorm(x, *ln), *dw)
+        else:
+            h = layernorm(dwconv_same(x, *dw), *ln)
+        h = linear(h, w1, _w(weights, l + ".pwconv1.bias"))
+        if MUTATION != "gelu_after":
+            h = codec_gelu(h)
+        h = linear(h, w2, _w(weights, l + ".pwconv2.bias"))
+        if MUTATION == "gelu_after":
+            h = codec_gelu(h)
+        x = h * _w(weights, l + ".gamma") if MUTATION == "no_residual" else x + h * _w(weights, l + ".gamma")
     x = layernorm(x, _w(weights, p + ".final_layer_norm.weight"), _w(weights, p + ".final_layer_norm.bias"))
     return linear(x, _w(weights, prefix + ".1.weight"), _w(weights, prefix + ".1.bias"))
 
@@ -120,4 +137,7 @@ def vocos(weights: Dict[str, np.ndarray], x: np.ndarray, prefix: str = "codec.de
 def decode(weights: Dict[str, np.ndarray], codes: Sequence[int], blocks: int = BLOCKS) -> np.ndarray:
     """[2T][1024] features of T codes (codec.cpp:64-72), float64."""
     hidden = vocos(weights, lookup(weights, codes), "codec.decoder", blocks)
-    return conv1d_same(nearest_up2(hidden), _w(weights, "codec.up.weight"), _w(weights, "codec.up.bias"))
+    up = (_w(weights, "codec.up.weight"), _w(weights, "codec.up.bias"))
+    if MUTATION == "up_after_conv":
+        return nearest_up2(conv1d_same(hidden, *up))
+    return conv1d_same(nearest_up2(hidden), *up)

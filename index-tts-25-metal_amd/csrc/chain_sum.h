@@ -11,8 +11,11 @@ namespace itts {
 namespace chain {
 
 // ((e[0] + e[1]) + e[2]) + ... + e[8193] in float, bit for bit the reference's index-order
-// chain (gpt_sampling.cpp:208), for e[j] >= 0 (or NaN), formed by one wave without 8194
-// dependent float adds.
+// chain (gpt_sampling.cpp:208), for e[j] >= 0 (+inf and NaN included), formed by one wave
+// without 8194 dependent float adds.
+// Once the running sum is NaN the chain stays NaN; once it is +inf it stays +inf unless a
+// later value is NaN.  Both are decided at the top of the loop, before the binade
+// arithmetic (which needs a finite sum).
 // While the running sum s stays in one binade [2^k, 2^(k+1)) (k >= -126; below 2^-125 the
 // spacing is the subnormal one, so s = 0 counts as k = -126), every representable value
 // there is a multiple of u = 2^(k-23), s = M u with M < 2^24 an integer, and float addition
@@ -65,6 +68,12 @@ __device__ inline float sum_wave(const float* __restrict__ e, int lane) {
     float s = 0.0f;
     int c = 0;
     while (c < kChunks) {
+        if (!(s <= 3.40282347e38f)) {  // NaN or +inf (the sum is never negative)
+            if (s != s) return s;
+            bool nan = false;
+            for (int j = 64 * c + lane; j < kMelVocab; j += 64) nan |= e[j] != e[j];
+            return __ballot(nan) ? __builtin_nanf("") : s;
+        }
         const int k = binade(s);
         const int sh = 23 - k;                                    // e / u = e * 2^sh
         uint32_t M = static_cast<uint32_t>(ldexpf(s, sh));        // s / u, an integer < 2^24

@@ -72,8 +72,9 @@ def test_strided_all_bit_patterns(itts, oracle, fn, name):
 
 def _chain_rows(seed):
     """Rows of 8194 non-negative floats: exp(x - max) of logit rows of several spreads, masked
-    and tied logits, all-equal rows, sums that start subnormal, and tie-heavy sequences of
-    short-mantissa powers of two (which put exact halves of the running sum's unit in play)."""
+    and tied logits, all-equal rows, sums that start subnormal, tie-heavy sequences of
+    short-mantissa powers of two (which put exact halves of the running sum's unit in play),
+    and rows holding NaN or +inf (the chain then ends NaN, or +inf with no NaN after it)."""
     rng = np.random.default_rng(seed)
     rows = []
     for sd in (0.5, 1.0, 3.0, 10.0, 40.0):
@@ -104,6 +105,18 @@ def _chain_rows(seed):
         v = np.ldexp(1.0 + rng.integers(0, 4, 8194) * 0.25, ex).astype(np.float32)
         v[rng.random(8194) < 0.2] = 0.0
         out.append(v)
+    # a NaN in the first, a middle and the last chunk; +inf alone, and +inf then a later NaN
+    base = out[3]
+    for idx in (5, 4100, 8193):
+        v = base.copy()
+        v[idx] = np.nan
+        out.append(v)
+    v = base.copy()
+    v[3000] = np.inf
+    out.append(v)
+    v = v.copy()
+    v[7000] = np.nan
+    out.append(v)
     return np.stack(out)
 
 
@@ -123,6 +136,9 @@ def test_beam_softmax_sum_is_the_index_order_chain(itts):
     st = itts._lib.itts_chain_sum_eval(v.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(vals),
                                        got.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
     assert st == 0
+    nan = np.isnan(exp)
+    assert nan.sum() == 4 and np.array_equal(np.isnan(got), nan), "NaN rows: the chain stays NaN"
+    got[nan] = exp[nan] = 0.0
     bad = np.nonzero(got.view(np.uint32) != exp.view(np.uint32))[0]
     print(f"chain sum: {len(bad)} of {len(vals)} rows differ", flush=True)
     assert len(bad) == 0, [(int(i), float(got[i]), float(exp[i])) for i in bad[:5]]

@@ -159,6 +159,11 @@ int itts_gpt_generate(itts_gpt* h, const float* prefix, uint32_t rows, const itt
 int itts_gpt_generate_noalloc(itts_gpt* h, const float* prefix, uint32_t rows, const itts_gen_options* options,
                               uint32_t max_tokens, uint32_t* codes_out, uint32_t* n_codes, int32_t* stopped);
 
+/* No counterpart in the reference: a diagnostic count, process-wide, of the device and
+ * pinned-host allocations and graph instantiations the GPT decoders have made.  A call that
+ * leaves it unchanged allocated nothing (the check on itts_gpt_generate_noalloc). */
+uint64_t itts_gpt_alloc_events(void);
+
 /* Independent requests decoded together (no reference counterpart: the reference
  * runs one request at a time, http.cpp:57).  Sequence b's prefix is prefixes[b]
  * (rows[b] x 1280); each follows generate()'s semantics with options[b].

@@ -12,6 +12,7 @@
 //     the graph with no per-token host work (the reference blocks per token:
 //     gpt.cpp:123 / metal_context.mm:4613-4630).
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdlib>
@@ -40,6 +41,10 @@ thread_local std::string g_create_error;
         if (e_ != hipSuccess) throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(e_) + " in " #x); \
     } while (0)
 
+// Every device or pinned allocation and every graph instantiation this file makes, counted
+// process-wide (itts_gpt_alloc_events): the check that an entry point allocates nothing.
+std::atomic<uint64_t> g_alloc_events{0};
+
 template <class T>
 struct DevBuf {
     T* p = nullptr;
@@ -55,7 +60,10 @@ struct DevBuf {
     }
     void alloc(size_t count) {
         reset();
-        if (count) HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
+        if (count) {
+            g_alloc_events.fetch_add(1, std::memory_order_relaxed);
+            HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
+        }
         n = count;
     }
     void ensure(size_t count) {
@@ -298,6 +306,7 @@ struct Engine {
     void init_common() {
         HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+        g_alloc_events.fetch_add(2, std::memory_order_relaxed);
         HIP_CHECK(hipHostMalloc(&pinned, 64 * sizeof(uint32_t), hipHostMallocDefault));
         HIP_CHECK(hipHostMalloc(&pinned_state, (kMaxBatch + 1) * sizeof(SeqState), hipHostMallocDefault));
         const size_t B = kMaxBatch;
@@ -709,6 +718,7 @@ struct Engine {
         }
         HIP_CHECK(hipStreamEndCapture(stream, &g));
         hipGraphExec_t exec = nullptr;
+        g_alloc_events.fetch_add(1, std::memory_order_relaxed);
         const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         HIP_CHECK(e);
@@ -1007,6 +1017,11 @@ struct Engine {
             throw std::runtime_error("itts_gpt_generate_noalloc: no scratch on this device" +
                                      (scratch_dev ? ": " + scratch_dev->error : std::string()));
         std::lock_guard<std::mutex> lock(*scratch_dev->lock);
+        struct Drain {  // destroyed before `lock`: on every exit, errors included, the work this
+                        // call queued on the shared scratch has finished before the lock is released
+            hipStream_t s;
+            ~Drain() { (void)hipStreamSynchronize(s); }
+        } drain{stream};
         uint8_t* base = scratch_dev->ptr;
         const PrefillBufs b{reinterpret_cast<float*>(base + kScratchOffX),      reinterpret_cast<float*>(base + kScratchOffXn),
                             reinterpret_cast<float*>(base + kScratchOffQ),      reinterpret_cast<float*>(base + kScratchOffAtt),
@@ -1459,6 +1474,7 @@ void Engine::generate_beams(const float* prefix, uint32_t rows, const itts_gen_o
     beam_np.ensure(1);
     beam_tmpl.ensure(1);
     if (!beam_ring) {
+        g_alloc_events.fetch_add(1, std::memory_order_relaxed);
         HIP_CHECK(hipHostMalloc(&beam_ring, kBeamRing * sizeof(BeamSlot), hipHostMallocDefault));
         HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&beam_ring_dev), beam_ring, 0));
         for (auto& e : bev) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -1629,6 +1645,8 @@ int guarded(itts_gpt* h, F&& f) {
 }  // namespace
 
 extern "C" {
+
+uint64_t itts_gpt_alloc_events(void) { return itts::g_alloc_events.load(std::memory_order_relaxed); }
 
 void itts_gen_options_default(itts_gen_options* o) {
     std::memset(o, 0, sizeof(*o));

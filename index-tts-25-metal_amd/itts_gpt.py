@@ -101,6 +101,7 @@ def _load() -> C.CDLL:
         "itts_gpt_state_release": (None, [P]),
         "itts_gpt_generate": (C.c_int, [P, f32p, u32, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
         "itts_gpt_generate_noalloc": (C.c_int, [P, f32p, u32, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
+        "itts_gpt_alloc_events": (C.c_uint64, []),
         "itts_gpt_generate_batch": (C.c_int, [P, u32, C.POINTER(f32p), u32p, C.POINTER(_Options), u32, u32p, u32p, C.POINTER(i32)]),
         "itts_gpt_generate_segments": (C.c_int, [P, f32p, f32p, u32p, u32p, u32, u32, C.POINTER(_Options), u32, u32p, u32p,
                                                  C.POINTER(i32)]),
@@ -570,6 +571,11 @@ def sample_gpt_token(processed: np.ndarray, rng_state: int, draws: int = 1):
 
 
 # ---------------------------------------------------------------------- synthetic inputs
+
+def alloc_events() -> int:
+    """itts_gpt_alloc_events: device/pinned allocations and graph instantiations made so far."""
+    return int(_lib.itts_gpt_alloc_events())
+
 
 def synthetic_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
     """Deterministic N(mean, std^2) values (Box-Muller over SplitMix64 keyed by (seed, index))."""

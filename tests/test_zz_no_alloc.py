@@ -43,6 +43,27 @@ def test_noalloc_codes_equal_generate(itts, small_weights, dtype):
     dec.close()
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_noalloc_allocates_nothing(itts, small_weights, dtype):
+    """itts_gpt_alloc_events counts every device and pinned allocation and every graph
+    instantiation the decoders make.  On a fresh decoder (no prefill yet, so generate() would
+    grow its prefill buffers to the prefix; for BF16 no decode graph captured yet), a no-alloc
+    call leaves the count unchanged.  generate() on the same input then moves it, which shows
+    the count sees those allocations; the codes are equal."""
+    dec = itts.GptDecoder(small_weights, kv_capacity=1024, weight_dtype=dtype)
+    prefix = itts.synthetic_normal(480 * 1280, 21, 0.0, 0.5)
+    o = itts.GenerationOptions(seed=5, suppress_stop=True)
+    before = itts.alloc_events()
+    a = dec.generate_noalloc(prefix, o, 40)
+    a2 = dec.generate_noalloc(prefix[: 300 * 1280], o, 20)
+    assert itts.alloc_events() == before, "a no-alloc call allocated"
+    b = dec.generate(prefix, o, 40)
+    assert itts.alloc_events() > before, "generate() grew nothing: the count does not see allocations"
+    assert (a.codes, a.stopped) == (b.codes, b.stopped)
+    assert a2.codes == dec.generate(prefix[: 300 * 1280], o, 20).codes
+    dec.close()
+
+
 def test_noalloc_prefill_state_continues_like_generate(itts, small_weights):
     """After generate_noalloc, step() continues from the same KV cache as after generate()."""
     dec = itts.GptDecoder(small_weights, kv_capacity=1024)

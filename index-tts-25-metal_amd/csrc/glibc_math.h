@@ -20,6 +20,26 @@
 // glibc: every float input of expf, every float-valued input of exp and every non-NaN input
 // of logf (tests/test_libm_repro.py on the CPU; the device on the GPU in
 // tests/test_gpu_libm.py).
+//
+// Attribution and licence of the restated method.  The structure, polynomial coefficients and
+// logf table below follow the ARM optimized-routines implementations of exp, expf and logf:
+//   Copyright (c) 2017-2018, Arm Limited.
+//   SPDX-License-Identifier: MIT
+//   Permission is hereby granted, free of charge, to any person obtaining a copy of this
+//   software and associated documentation files (the "Software"), to deal in the Software
+//   without restriction, including without limitation the rights to use, copy, modify, merge,
+//   publish, distribute, sublicense, and/or sell copies of the Software, and to permit persons
+//   to whom the Software is furnished to do so, subject to the following conditions: the above
+//   copyright notice and this permission notice shall be included in all copies or substantial
+//   portions of the Software.  THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND,
+//   EXPRESS OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY, FITNESS
+//   FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT.  IN NO EVENT SHALL THE AUTHORS OR COPYRIGHT
+//   HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF
+//   CONTRACT, TORT OR OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE
+//   USE OR OTHER DEALINGS IN THE SOFTWARE.
+// glibc (2.28 and later) ships the same routines under the LGPL-2.1-or-later with that
+// attribution ("Contributed by Szabolcs Nagy, ARM"); the tables of 2^(i/N) here were computed
+// from their definition, not taken from either source.
 #pragma once
 #include <stdint.h>
 

@@ -137,7 +137,78 @@ int run_bundle(const char* path, bool ref_style) {
     return run_bundle_with(w);
 }
 
+// `gpt_shim_example gpt_test <model bundle> <fixture bundle>`: the reference's gpt_test
+// (src/main.cpp:31-66) as a caller of this drop-in: the model and its single-file fixture
+// through BundleWeights (Weights(model), fixture(golden, false)), then prepare for five
+// languages, prefill, four steps, greedy and 3-beam generation, each compared with the
+// fixture the way main.cpp's compare (19-30) and check_logits (40-47) do.  One JSON line
+// per case, as gpt_test prints them; exit status 0 when every case passes.
+bool compare(const std::string& name, const std::vector<float>& actual, const std::vector<float>& expected,
+             float tolerance = 1e-4f, double rms_tolerance = 1e-5) {
+    if (actual.size() != expected.size()) throw std::runtime_error("Output shape mismatch: " + name);
+    double sum = 0, square = 0;
+    float peak = 0;
+    for (size_t i = 0; i < actual.size(); i++) {
+        if (!std::isfinite(actual[i]) || !std::isfinite(expected[i])) throw std::runtime_error("Non-finite output: " + name);
+        const auto d = std::abs(actual[i] - expected[i]);
+        peak = std::max(peak, d);
+        sum += d;
+        square += d * d;
+    }
+    const double mean = sum / actual.size(), rmse = std::sqrt(square / actual.size());
+    const bool pass = peak < tolerance && rmse < rms_tolerance;
+    std::printf("{\"case\":\"%s\",\"max_abs_error\":%g,\"mean_abs_error\":%g,\"rmse\":%g,\"pass\":%s}\n", name.c_str(), peak, mean,
+                rmse, pass ? "true" : "false");
+    return pass;
+}
+
+int run_gpt_test(const char* model, const char* golden) {
+    itts25::BundleWeights weights(model), fixture(golden, false);
+    DeviceContext metal;
+    itts25::GptDecoder gpt(weights, metal);
+    bool pass = true;
+    std::vector<float> chinese;
+    for (const auto* lang : {"ZH", "EN", "JA", "ES", "AR"}) {
+        const auto name = std::string("prefix.") + lang;
+        auto prefix = gpt.prepare(fixture.get("speaker"), fixture.get("emotion"), fixture.ids(name + ".tokens"),
+                                  fixture.ids(name + ".language")[0]);
+        pass = compare(name, prefix, fixture.get(name + ".embeddings")) && pass;
+        if (std::string(lang) == "ZH") chinese = std::move(prefix);
+    }
+    auto check_logits = [&](const std::string& name, const std::vector<float>& logits) {
+        const auto& ref = fixture.get(name + ".logits");
+        auto argmax = [](const std::vector<float>& x) { return std::max_element(x.begin(), x.end()) - x.begin(); };
+        const bool match = argmax(logits) == argmax(ref);
+        std::printf("{\"case\":\"%s.argmax\",\"exact_match\":%s}\n", name.c_str(), match ? "true" : "false");
+        return compare(name, logits, ref, 1e-4f, 2e-5) && match;
+    };
+    pass = check_logits("decode.prefill", gpt.prefill(chinese)) && pass;
+    for (uint32_t i = 1; i <= 4; i++) {
+        auto name = "decode." + std::to_string(i);
+        pass = check_logits(name, gpt.step(fixture.ids(name + ".code")[0], i)) && pass;
+    }
+    itts25::GenerationOptions config;
+    config.do_sample = false;
+    config.repetition_penalty = 1;
+    auto generated = gpt.generate(chinese, config, 8);
+    auto expected_codes = fixture.ids("generation.greedy.codes");
+    if (!expected_codes.empty() && expected_codes.back() == 8193) expected_codes.pop_back();
+    const bool generated_match = generated.codes == expected_codes;
+    pass = generated_match && pass;
+    std::printf("{\"case\":\"generation.greedy\",\"exact_match\":%s}\n", generated_match ? "true" : "false");
+    config.num_beams = 3;
+    auto beam = gpt.generate(chinese, config, 8);
+    auto expected_beam = fixture.ids("generation.beam.codes");
+    if (!expected_beam.empty() && expected_beam.back() == 8193) expected_beam.pop_back();
+    const bool beam_match = beam.codes == expected_beam;
+    pass = beam_match && pass;
+    std::printf("{\"case\":\"generation.beam\",\"exact_match\":%s}\n", beam_match ? "true" : "false");
+    std::printf("{\"stage\":\"gpt_2.5\",\"cached_tokens\":%u,\"pass\":%s}\n", gpt.cached_tokens(), pass ? "true" : "false");
+    return pass ? 0 : 1;
+}
+
 int main(int argc, char** argv) {
+    if (argc >= 4 && std::strcmp(argv[1], "gpt_test") == 0) return run_gpt_test(argv[2], argv[3]);
     if (argc >= 3 && std::strcmp(argv[1], "bundle") == 0) return run_bundle(argv[2], false);
     if (argc >= 3 && std::strcmp(argv[1], "refbundle") == 0) return run_bundle(argv[2], true);
     if (argc >= 4 && std::strncmp(argv[1], "qwen", 4) == 0) {

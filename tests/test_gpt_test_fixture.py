@@ -110,3 +110,25 @@ def test_gpt_test_sequence_on_the_hip_path(itts):
     assert ok and greedy_match and beam_match
     gpt.close()
     fx.close()
+
+
+@pytest.mark.gpu
+def test_gpt_test_through_the_cpp_dropin(itts, tmp_path):
+    """The same sequence written as gpt_test writes it, in C++ against the drop-in
+    (index-tts-25-metal_amd/cpp/gpt_shim_example.cpp, mode gpt_test): the model as a MIT2
+    directory bundle (target index-tts2.5) and the fixture through BundleWeights."""
+    import json
+    import subprocess
+
+    import make_gpt_test_fixture as mk
+
+    exe = ROOT / "index-tts-25-metal_amd" / "cpp" / "gpt_shim_example"
+    assert exe.exists(), "shim example not built"
+    print("gpt_test (C++): writing the model bundle", flush=True)
+    model = itts.write_mit2_bundle(tmp_path / "model", mk.model())
+    out = subprocess.run([str(exe), "gpt_test", str(model), str(FIXTURE)], capture_output=True, text=True, timeout=600)
+    print(out.stdout, flush=True)
+    lines = [json.loads(l) for l in out.stdout.splitlines() if l.startswith("{")]
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert lines[-1]["stage"] == "gpt_2.5" and lines[-1]["pass"] is True
+    assert sum(1 for l in lines if "max_abs_error" in l) == 10 and all(l.get("pass", True) for l in lines)

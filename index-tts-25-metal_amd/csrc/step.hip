@@ -498,6 +498,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = l > 0;
             }
             XRead<5> xr;
+            if (l > 0) poll_delay();
             xr.issue(XB, idx, use, ep(l, kEpXh));
             LnParDot ln;
             ln.load(par + kParLn1W, par + kParLn1B, lane);
@@ -780,6 +781,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = true;
             }
             XRead<5> xr;
+            poll_delay();
             xr.issue(XB, idx, use, ep(l, kEpAttn));
             LaneBias<kGProj, false> bias;
             bias.load(par + kParProjB + P.p0, P.pn, wave, lane);
@@ -815,6 +817,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = true;
             }
             XRead<5> xr;
+            poll_delay();
             xr.issue(XB, idx, use, ep(l, kEpHmid));
             LnParDot ln;
             ln.load(par + kParLn2W, par + kParLn2B, lane);
@@ -856,6 +859,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
                 use[i] = true;
             }
             XRead<NF> xr;
+            poll_delay();
             xr.issue(XB, idx, use, ep(l, kEpFf));
             LaneBias<kGFc2, true> bias;
             bias.load(par + kParFc2B + P.g0, P.gn, wave, lane);
@@ -893,6 +897,7 @@ __global__ __launch_bounds__(kST) void step_kernel(StepArgs a) {
             use[i] = true;
         }
         XRead<5> xr;
+        poll_delay();
         xr.issue(XB, idx, use, ep(a.layers, kEpXh));
         LnPar lf;
         lf.load(a.head + kHeadLnfW, a.head + kHeadLnfB, tid);

@@ -26,6 +26,14 @@ constexpr int kCachePolicyNt = 2;     // cache-policy operand: nt
 constexpr int kBufferDword3 = 0x00020000;  // descriptor word 3 of a raw 32-bit buffer on gfx9
 constexpr int kKvRowsPerChunk = kChunkF / kHeadDim;  // 20 cached rows of one head
 constexpr unsigned kSpinLimit = 1u << 20;     // global polls (~1 us each)
+// Sleep (64 * kPollDelay clocks, about 0.5 us) before a phase's first poll of its input
+// vector.  The producers of that vector finish 1-3 us after this workgroup ends its own
+// previous phase, and every poll round is a memory-side request per element still missing,
+// so rounds issued before the data can exist only add to the queues that the hand-offs and
+// the weight stream share (one more unit of hand-off polling made a 752-row step 18% slower).
+// Measured (step at 752 cached rows): no sleep 624 us, 8 -> 607, 20 -> 587, 28 -> 594,
+// 40 -> 611; a sleep before the attention tiles' q poll and the merge's poll gained nothing.
+constexpr int kPollDelay = 20;
 constexpr unsigned kLdsSpinLimit = 1u << 24;  // LDS polls (~0.1 us each)
 static_assert(kCW == 4 && kLW == 4, "role split");
 
@@ -99,6 +107,8 @@ __device__ __forceinline__ void xread(const uint64_t* base, const int (&idx)[N],
     r.issue(base, idx, use, e);
     r.wait(base, idx, e, out, err, failed);
 }
+
+__device__ __forceinline__ void poll_delay() { __builtin_amdgcn_s_sleep(kPollDelay); }
 
 // A wave-uniform value through an empty asm: conditions derived from it are formed where
 // they are used instead of being hoisted out of the layer loop into spilled registers.

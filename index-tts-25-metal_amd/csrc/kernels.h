@@ -132,11 +132,13 @@ constexpr int kStepThreads = 512;
 constexpr int kStepExchange = kWidth + kQkv + kWidth + kWidth + kFfn + kHeads * kAttnMaxSplits * 68 + kMelVocab;
 // The vectors every workgroup reads (h, q|k|v, attention output, hmid, FFN activations:
 // the first kStepBroadcast slots) are also written to kStepCopies - 1 further copies
-// after the kStepExchange slots, kStepCopyStride apart, and workgroup b reads copy b % 4:
-// 65 536 polling threads then spread over four sets of memory channels instead of one
-// (measured: 4 copies 2-4% faster per step than 1, 8 no better than 4).
+// after the kStepExchange slots, kStepCopyStride apart, and workgroup b reads copy
+// b % kStepCopies, so the polling threads spread over more memory channels.  Measured at
+// 752 cached rows: polling from a phase's first cycle, 4 copies were 2-4% faster per step
+// than 1 and 8 no better than 4; with the poll delay (step_common.h) 2 copies take 580 us,
+// 1 copy 580-581 and 4 copies 591 (fewer stores per value), and the batch step is no slower.
 constexpr int kStepBroadcast = kWidth + kQkv + kWidth + kWidth + kFfn;
-constexpr int kStepCopies = 4;
+constexpr int kStepCopies = 2;
 constexpr int kStepCopyStride = kStepBroadcast + 256;
 constexpr size_t kStepExchangeTotal = size_t(kStepExchange) + size_t(kStepCopies - 1) * kStepCopyStride;
 

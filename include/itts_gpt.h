@@ -222,7 +222,10 @@ int itts_gpt_last_timing(const itts_gpt* h, itts_gpt_timing* out);
  * 2 mlp.c_fc GEMV (+LayerNorm, GELU), 3 mlp.c_proj GEMV (+residual), 4 mel_head GEMV
  * (+ln_f, final_norm), 5 decode attention, 6 the persistent whole-step kernel (batch 1,
  * FP32 weights only), 7 a 256 MiB device-to-device copy (reference for traffic counters).
- * Attention and the step kernel run with `cached_rows` rows in the cache (0 -> 752). */
+ * Attention and the step kernel run with `cached_rows` rows in the cache (0 -> 752).
+ * which | ITTS_BENCH_ONE_LAYER: every launch uses layer 0's weights, so after the first
+ * launch they are served from the memory-side cache (the cost of a launch without HBM). */
+#define ITTS_BENCH_ONE_LAYER 0x100
 int itts_gpt_bench_kernel(itts_gpt* h, int32_t which, uint32_t batch, uint32_t cached_rows, uint32_t iters, float* avg_ms,
                           double* bytes_per_launch);
 

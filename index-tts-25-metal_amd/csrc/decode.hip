@@ -81,10 +81,6 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = (blockIdx.x * NW + wave) * RPW;
 
-    bool any = false;
-    for (int b = 0; b < a.nseq; ++b) any |= a.state[b].active != 0;
-    if (!any) return;
-
     // Prologue input first, so waiting on it does not wait on the weight stream.
     float hv[B][PER];
     if constexpr (PRO == kProLn || PRO == kProLn2) {
@@ -151,6 +147,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
         const int rr = row < a.rows ? row : a.rows - 1;  // clamp: loads stay in bounds, result discarded
 #pragma unroll
         for (int j = 0; j < J; ++j) wv[r][j] = LD::load(w, static_cast<size_t>(rr) * (COLS / 4) + j * 64 + lane);
+    }
+    // Whether any sequence is still decoding, read only now that the weights are requested:
+    // a live step's weight loads then never wait for this round trip.  A replay after every
+    // sequence finished still streams the weights once, but stores nothing.
+    {
+        uint32_t any = 0;
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            if (b < a.nseq) any |= a.state[b].active;
+        if (!any) return;
     }
 
     __shared__ float xs[PRO == kProNone ? 4 : (STAGED && COLS > kWidth ? 2 : 1) * B * kWidth];

@@ -1179,6 +1179,8 @@ struct Engine {
     // Launches one decode kernel kind `iters` times (layer l = i % layers, so consecutive
     // launches stream different weights) between two HIP events on the handle's stream.
     void bench_kernel(int which, int batch, uint32_t cached_rows, int iters, float* avg_ms, double* bytes) {
+        const bool one_layer = (which & ITTS_BENCH_ONE_LAYER) != 0;  // every launch on layer 0's weights
+        which &= ~ITTS_BENCH_ONE_LAYER;
         if (!layers || which < 0 || which > 7 || iters < 1 || batch < 1 || batch > static_cast<int>(max_batch))
             throw std::invalid_argument("Invalid kernel benchmark request");
         if (which == 6 && !persistent(batch, false)) throw std::invalid_argument("The persistent step kernel is not available on this decoder");
@@ -1239,9 +1241,9 @@ struct Engine {
                 }
             }
         };
-        for (int i = 0; i < std::min(iters, layers); ++i) launch(i % layers);  // warm-up
+        for (int i = 0; i < std::min(iters, layers); ++i) launch(one_layer ? 0 : i % layers);  // warm-up
         HIP_CHECK(hipEventRecord(ev[0], stream));
-        for (int i = 0; i < iters; ++i) launch(i % layers);
+        for (int i = 0; i < iters; ++i) launch(one_layer ? 0 : i % layers);
         HIP_CHECK(hipEventRecord(ev[1], stream));
         HIP_CHECK(hipEventSynchronize(ev[1]));
         float ms = 0;

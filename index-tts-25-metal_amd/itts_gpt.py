@@ -512,12 +512,14 @@ class GptDecoder:
 
     KERNELS = ("gemv_c_attn", "gemv_attn_proj", "gemv_c_fc", "gemv_mlp_proj", "gemv_mel_head", "attention", "step", "copy")
 
-    def bench_kernel(self, which: str, iters: int = 240, batch: int = 1, cached_rows: int = 0) -> dict:
+    def bench_kernel(self, which: str, iters: int = 240, batch: int = 1, cached_rows: int = 0, one_layer: bool = False) -> dict:
         """Mean duration (HIP events, back-to-back launches) and algorithmic bytes of one decode
-        kernel kind; attention and "step" run with `cached_rows` cached rows (0 -> 752)."""
+        kernel kind; attention and "step" run with `cached_rows` cached rows (0 -> 752).
+        one_layer: every launch on layer 0's weights (served from the memory-side cache)."""
         ms = C.c_float()
         by = C.c_double()
-        self._check(_lib.itts_gpt_bench_kernel(self._h, self.KERNELS.index(which), int(batch), int(cached_rows), int(iters),
+        kind = self.KERNELS.index(which) | (0x100 if one_layer else 0)
+        self._check(_lib.itts_gpt_bench_kernel(self._h, kind, int(batch), int(cached_rows), int(iters),
                                                C.byref(ms), C.byref(by)))
         return {"avg_ms": float(ms.value), "bytes": float(by.value)}
 

@@ -350,11 +350,20 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, 
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     int off[kMaxBatch + 1];  // first tile of each sequence
     int Ls[kMaxBatch];
+    // Every sequence's flag and length requested at once (slots past nseq read slot 0's, then
+    // ignored), so the tile walk waits for one round trip instead of one per sequence.
+    uint32_t act[kMaxBatch], cached[kMaxBatch];
+#pragma unroll
+    for (int b = 0; b < kMaxBatch; ++b) {
+        const int bb = b < a.nseq ? b : 0;
+        act[b] = a.state[bb].active;
+        cached[b] = a.state[bb].n;
+    }
     off[0] = 0;
 #pragma unroll
     for (int b = 0; b < kMaxBatch; ++b) {
-        const bool live = b < a.nseq && a.state[b].active;
-        Ls[b] = live ? static_cast<int>(a.state[b].n) + 1 : 0;  // cached rows + the row appended by this step
+        const bool live = b < a.nseq && act[b] != 0;
+        Ls[b] = live ? static_cast<int>(cached[b]) + 1 : 0;  // cached rows + the row appended by this step
         off[b + 1] = off[b] + (live ? kHeads * live_splits(Ls[b], a.splits) : 0);
     }
     for (int t = blockIdx.x; t < off[kMaxBatch]; t += gridDim.x) {

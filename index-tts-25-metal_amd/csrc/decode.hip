@@ -148,6 +148,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int j = 0; j < J; ++j) wv[r][j] = LD::load(w, static_cast<size_t>(rr) * (COLS / 4) + j * 64 + lane);
     }
+    // The epilogue's (row, sequence) pair of this lane (see the wave_sum4 layout below), and its
+    // bias and residual, requested behind the weights so the epilogue does not wait for them.
+    constexpr int NV = RPW * B, NK = (NV + 3) / 4;
+    const int lw = lane & 15, lg = lane >> 4;
+    const int i = 4 * lw + ((lg == 1) ? 2 : (lg == 2) ? 1 : lg);
+    const int er = (i < NV ? i : 0) / B, eb = (i < NV ? i : 0) % B;
+    const int erow = min(row0 + er, a.rows - 1);  // in bounds; unused when past the rows
+    const float ebias = a.bias[erow];
+    float eresid = 0.0f;
+    if constexpr (EPI == kEpiResid) eresid = a.resid[eb * a.out_stride + erow];
     // Whether any sequence is still decoding, read only now that the weights are requested:
     // a live step's weight loads then never wait for this round trip.  A replay after every
     // sequence finished still streams the weights once, but stores nothing.
@@ -279,21 +289,18 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     // sum is bitwise the one wave_sum gives.  Lane L then owns accumulator
     // i = 4 (L & 15) + {0, 2, 1, 3}[L >> 4] (one (row, sequence) pair per lane, no loop over
     // the pairs).
-    constexpr int NV = RPW * B, NK = (NV + 3) / 4;
-    auto accv = [&](int i) -> float { return i < NV ? acc[i / B][i % B] : 0.0f; };
+    auto accv = [&](int k) -> float { return k < NV ? acc[k / B][k % B] : 0.0f; };
     float red4[NK];
 #pragma unroll
     for (int k = 0; k < NK; ++k) red4[k] = wave_sum4(accv(4 * k), accv(4 * k + 1), accv(4 * k + 2), accv(4 * k + 3));
-    const int lw = lane & 15, lg = lane >> 4;
-    const int i = 4 * lw + ((lg == 1) ? 2 : (lg == 2) ? 1 : lg);
     float sum = red4[0];
 #pragma unroll
     for (int k = 1; k < NK; ++k) sum = lw == k ? red4[k] : sum;
     if (lw >= NK || i >= NV) return;
-    const int r = i / B, b = i % B;
-    const int row = row0 + r;
+    const int b = eb;
+    const int row = row0 + er;
     if (row >= a.rows) return;
-    const float v = sum + a.bias[row];
+    const float v = sum + ebias;
     if constexpr (EPI == kEpiQkv) {
         if (row < kWidth) {
             a.q[b * kWidth + row] = v;
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
             a.kv[off] = v;
         }
     } else if constexpr (EPI == kEpiResid) {
-        a.out[b * a.out_stride + row] = a.resid[b * a.out_stride + row] + v;
+        a.out[b * a.out_stride + row] = eresid + v;
     } else if constexpr (EPI == kEpiGelu) {
         a.out[b * a.out_stride + row] = gelu_f(v);
     } else {

@@ -28,11 +28,8 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     __shared__ float wred[NWAVE];
     __shared__ float log_sum_s;
     const int p = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    if (a.parents_dev && p >= static_cast<int>(*a.parents_dev)) {  // the whole workgroup leaves together
-        if (t == 0) a.status[1 + p] = kOk;
-        return;
-    }
-    const float* lg = a.logits + static_cast<size_t>(p) * V;
+    const float* lg = a.logits + static_cast<size_t>(p) * V;  // rows < parents: in bounds
+    uint32_t hits;
     float* e = reinterpret_cast<float*>(sm.sortbuf) + V + 2;  // after s[] inside the union, 16-byte aligned
     static_assert(V + 2 + chain::kPad <= kSortMax * 2, "the padded exponentials fit in the sort buffer");
     float mloc = -INFINITY;
@@ -42,6 +39,23 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
         for (int q = 0; q < IPT; ++q) {
             const int i = t + q * NT;
             v[q] = i < V ? lg[i] : -INFINITY;
+        }
+        // the parent's repetition set, behind the logits: the log-softmax hides its round trip
+        hits = 0;
+        if (a.penalty != 1.0f) {
+            uint8_t hit[IPT];
+#pragma unroll
+            for (int q = 0; q < IPT; ++q) {
+                const int i = t + q * NT;
+                hit[q] = i < V ? a.seen[static_cast<size_t>(p) * V + i] : 0;
+            }
+#pragma unroll
+            for (int q = 0; q < IPT; ++q) hits |= hit[q] ? 1u << q : 0u;
+        }
+        // this step's parent count, read behind the loads above
+        if (a.parents_dev && p >= static_cast<int>(*a.parents_dev)) {  // the whole workgroup leaves together
+            if (t == 0) a.status[1 + p] = kOk;
+            return;
         }
 #pragma unroll
         for (int q = 0; q < IPT; ++q) {
@@ -69,8 +83,20 @@ __global__ __launch_bounds__(NT) void beam_scores_kernel(BeamArgs a) {
     const float log_sum = log_sum_s;
     for (int i = t; i < V; i += NT) sm.s[i] = sm.s[i] - log_sum;
     __syncthreads();
+    // The repetition penalty (gpt_sampling.cpp:33-49) here, from the bits read at the start;
+    // run_processors then goes on with the temperature (the same operations in the same order).
+    if (a.penalty != 1.0f) {
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V && ((hits >> q) & 1u)) {
+                const float v = sm.s[i];
+                sm.s[i] = v < 0.0f ? v * a.penalty : v / a.penalty;
+            }
+        }  // each thread's own entries, which run_processors reads in the same thread
+    }
     bool topp = false;
-    const uint32_t st = run_processors(sm, a.seen + static_cast<size_t>(p) * V, a.penalty, a.temperature, a.top_k, a.top_p,
+    const uint32_t st = run_processors(sm, a.seen + static_cast<size_t>(p) * V, 1.0f, a.temperature, a.top_k, a.top_p,
                                        a.num_beams, a.probs + static_cast<size_t>(p) * V, true, &topp);
     if (t == 0) a.status[1 + p] = st;
     if (st != kOk) return;
@@ -186,7 +212,7 @@ __device__ uint32_t block_scan(uint32_t c, uint32_t* wtot, uint32_t* total) {
 // Returns kOk or the failing status; ids[0..take) on success.
 constexpr int kLdsCands = 2048;
 __device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, double* pw, double* pre, uint32_t F, int take, uint64_t& rng,
-                                         uint32_t* ids) {
+                                         uint32_t* ids, float* idsc) {
     const int lane = threadIdx.x & 63;
     constexpr uint32_t kTaken = 0x80000000u;
     constexpr uint32_t kNone = 0xffffffffu;
@@ -247,6 +273,7 @@ __device__ uint32_t draw_candidates_wave(uint32_t* lid, const float* lsc, double
         if (pick == kNone) pick = last;
         if (lane == 0) {
             ids[d] = lid[pick];
+            idsc[d] = lsc[pick];
             lid[pick] |= kTaken;
             pw[pick] = 0.0;
         }
@@ -303,12 +330,31 @@ __device__ uint32_t finite_in_order(const float* S, uint32_t* wtot, uint32_t* li
     return F;
 }
 
+// Stable sort of (ids, scores)[0..n) by score, descending (insertion sort, one thread): the
+// reference is built with libc++, whose std::sort keeps equal candidates in order below 24
+// elements (n <= 20).  The scores are the chosen ids' own, held in LDS beside them.
+__device__ __forceinline__ void stable_sort_desc(uint32_t* ids, float* sc, int n) {
+    for (int x = 1; x < n; ++x) {
+        const uint32_t v = ids[x];
+        const float sv = sc[x];
+        int y = x - 1;
+        while (y >= 0 && sc[y] < sv) {
+            ids[y + 1] = ids[y];
+            sc[y + 1] = sc[y];
+            --y;
+        }
+        ids[y + 1] = v;
+        sc[y + 1] = sv;
+    }
+}
+
 __device__ __forceinline__ void select_candidates(const BeamArgs& a) {
     __shared__ uint32_t hist[256], sel[2], wtot[NWAVE];
     __shared__ uint32_t lid[kLdsCands];
     __shared__ float lsc[kLdsCands];
     __shared__ __align__(16) double pw[kLdsCands], pre[kLdsCands];
     __shared__ uint32_t ids[2 * kMaxBeamTake];
+    __shared__ float idsc[2 * kMaxBeamTake];  // the score of each chosen id (sorted with it)
     __shared__ float wmax[NWAVE];
     __shared__ float mx_s;
     __shared__ uint32_t stop_s;
@@ -337,16 +383,21 @@ __device__ __forceinline__ void select_candidates(const BeamArgs& a) {
             }
         });
         __syncthreads();
+        if (t < take) idsc[t] = S[ids[t]];  // one parallel read; the sort compares in LDS
+        __syncthreads();
         if (t == 0) {
             // (score desc, index asc): the order std::partial_sort produces with index ties.
             for (int x = 1; x < take; ++x) {
                 const uint32_t v = ids[x];
+                const float sv = idsc[x];
                 int y = x - 1;
-                while (y >= 0 && (S[ids[y]] < S[v] || (S[ids[y]] == S[v] && ids[y] > v))) {
+                while (y >= 0 && (idsc[y] < sv || (idsc[y] == sv && ids[y] > v))) {
                     ids[y + 1] = ids[y];
+                    idsc[y + 1] = idsc[y];
                     --y;
                 }
                 ids[y + 1] = v;
+                idsc[y + 1] = sv;
             }
             a.status[0] = kOk;
         }
@@ -381,29 +432,19 @@ __device__ __forceinline__ void select_candidates(const BeamArgs& a) {
         if (F <= static_cast<uint32_t>(kLdsCands)) {
             if (wave != 0) return;
             uint64_t rng = *a.rng;
-            const uint32_t st = draw_candidates_wave(lid, lsc, pw, pre, F, take, rng, ids);
+            const uint32_t st = draw_candidates_wave(lid, lsc, pw, pre, F, take, rng, ids, idsc);
             if (st != kOk) {
                 if (t == 0) a.status[0] = st;
                 return;
             }
             if (t == 0) {
                 *a.rng = rng;
-                // Stable sort by score, descending: the reference is built with libc++, whose std::sort
-                // keeps equal candidates in order below 24 elements (take <= 20).
-                for (int x = 1; x < take; ++x) {
-                    const uint32_t v = ids[x];
-                    int y = x - 1;
-                    while (y >= 0 && S[ids[y]] < S[v]) {
-                        ids[y + 1] = ids[y];
-                        --y;
-                    }
-                    ids[y + 1] = v;
-                }
+                stable_sort_desc(ids, idsc, take);
                 a.status[0] = kOk;
             }
             if (t < take) {
                 const uint32_t id = ids[t];
-                a.cand[t] = BeamCand{id / static_cast<uint32_t>(V), id % static_cast<uint32_t>(V), S[id], 0u};
+                a.cand[t] = BeamCand{id / static_cast<uint32_t>(V), id % static_cast<uint32_t>(V), idsc[t], 0u};
             }
             return;
         }
@@ -464,25 +505,17 @@ __device__ __forceinline__ void select_candidates(const BeamArgs& a) {
                 return;
             }
         }
+        if (t < take) idsc[t] = S[ids[t]];
+        __syncthreads();
         if (t == 0) {
             *a.rng = rng;
-            // Stable sort by score, descending: the reference is built with libc++, whose std::sort
-            // keeps equal candidates in order below 24 elements (take <= 20).
-            for (int x = 1; x < take; ++x) {
-                const uint32_t v = ids[x];
-                int y = x - 1;
-                while (y >= 0 && S[ids[y]] < S[v]) {
-                    ids[y + 1] = ids[y];
-                    --y;
-                }
-                ids[y + 1] = v;
-            }
+            stable_sort_desc(ids, idsc, take);
             a.status[0] = kOk;
         }
     }
     if (t < take) {
         const uint32_t id = ids[t];
-        a.cand[t] = BeamCand{id / static_cast<uint32_t>(V), id % static_cast<uint32_t>(V), S[id], 0u};
+        a.cand[t] = BeamCand{id / static_cast<uint32_t>(V), id % static_cast<uint32_t>(V), idsc[t], 0u};
     }
 }
 

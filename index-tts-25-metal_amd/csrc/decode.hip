@@ -348,6 +348,7 @@ hipError_t launch_gemv(const GemvArgs& a, int batch, bool bf16, hipStream_t s) {
 // ------------------------------------------------------------------ attention
 
 // One (sequence b, head h, split s) tile of the split pass.
+template <int PER>
 __device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, int s, int L, int S);
 
 // The grid is a fixed kAttnGrid workgroups (a captured graph replays it whatever the cache
@@ -378,11 +379,18 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int q = 1; q < kMaxBatch; ++q) b += t >= off[q] ? 1 : 0;
         const int r = t - off[b];
-        attention_tile(a, b, r % kHeads, r / kHeads, Ls[b], live_splits(Ls[b], a.splits));
+        const int S = live_splits(Ls[b], a.splits);
+        // Tiles of at most 64 rows (every cache up to 768 rows) run the code with 4 row slots per
+        // 16-lane group; the other slots' zero weights would leave every sum unchanged.
+        if ((Ls[b] + S - 1) / S <= 64)
+            attention_tile<kAttnMaxChunk / 32>(a, b, r % kHeads, r / kHeads, Ls[b], S);
+        else
+            attention_tile<kAttnMaxChunk / 16>(a, b, r % kHeads, r / kHeads, Ls[b], S);
         __syncthreads();  // the tile's LDS (redm, reds, accs) is reused by the next one
     }
 }
 
+template <int PER>
 __device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, int s, int L, int S) {
     const int chunk = (L + S - 1) / S;
     const int p0 = s * chunk;
@@ -390,18 +398,30 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, 
     const int t = threadIdx.x, g = t >> 4, sub = t & 15, lane = t & 63, wave = t >> 6;
     const float4 q4 = *reinterpret_cast<const float4*>(a.q + b * kWidth + h * kHeadDim + sub * 4);
 
-    constexpr int PER = kAttnMaxChunk / 16;
+    // Every row's owner slot (beams) is requested before any K/V load, and no load sits under a
+    // per-row branch: rows past the tile read its first row (in bounds) and are zeroed after.  The K/V
+    // address of a row depends on its owner and loads complete in order, so reading the owner
+    // row by row made each row wait for every earlier row's K/V as well (one memory round trip
+    // per row); the branches around the loads also cost waits for reused registers.
+    const int pz = p0 < L ? p0 : L - 1;  // a row of the cache (the tile's first)
+    uint32_t slot[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int p = p0 + g + 16 * i, pc = p < p1 ? p : pz;
+        slot[i] = a.table ? a.table[static_cast<size_t>(b) * a.kv_cap + pc] : static_cast<uint32_t>(b);
+    }
     float4 k4[PER], v4[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int p = p0 + g + 16 * i;
-        if (p < p1) {
-            const uint32_t slot = a.table ? a.table[static_cast<size_t>(b) * a.kv_cap + p] : static_cast<uint32_t>(b);
-            const size_t base = static_cast<size_t>(slot) * a.kv_slot_stride + a.kv_layer_off +
-                                (static_cast<size_t>(h) * a.kv_cap + p) * kHeadDim + sub * 4;
-            k4[i] = *reinterpret_cast<const float4*>(a.kv + base);
-            v4[i] = *reinterpret_cast<const float4*>(a.kv + base + a.kv_v_off);
-        } else {
+        const int p = p0 + g + 16 * i, pc = p < p1 ? p : pz;
+        const size_t base = static_cast<size_t>(slot[i]) * a.kv_slot_stride + a.kv_layer_off +
+                            (static_cast<size_t>(h) * a.kv_cap + pc) * kHeadDim + sub * 4;
+        k4[i] = *reinterpret_cast<const float4*>(a.kv + base);
+        v4[i] = *reinterpret_cast<const float4*>(a.kv + base + a.kv_v_off);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        if (!(p0 + g + 16 * i < p1)) {
             k4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             v4[i] = k4[i];
         }

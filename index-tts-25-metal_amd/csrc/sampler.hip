@@ -9,7 +9,7 @@ using namespace sampling;
 
 __global__ __launch_bounds__(NT) void sampler_kernel(SampleArgs a) {
     __shared__ Smem sm;
-    sample_sequence(sm, a, blockIdx.x);
+    sample_sequence<NT, true>(sm, a, blockIdx.x);
 }
 
 }  // namespace

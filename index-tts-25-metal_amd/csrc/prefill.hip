@@ -17,6 +17,8 @@
 // Rows of several sequences may be stacked (ragged batch prefill): row m belongs to
 // cache slot row_slot[m] at position row_pos[m] and attends to that slot's rows
 // 0..row_pos[m].
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace itts {
@@ -221,6 +223,62 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
                 const float u = __shfl_xor(v, 1, 64);
                 if (row < mrows && !(col & 1)) a.c[static_cast<size_t>(m0 + row) * (a.N / 2) + col / 2] = swiglu_f(v, u);
             }
+    } else if constexpr (EPI == kGemmResid) {
+        // Every row's residual requested before the first store (rows past the block read the
+        // block's first row): a load under the per-row branch was waited for before the next.
+        const float bias = a.bias[col];
+        float res[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = (t0 + 2 * t) * 16 + rq + r;
+                res[t][r] = a.c[static_cast<size_t>(m0 + (row < mrows ? row : 0)) * a.N + col];
+            }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = (t0 + 2 * t) * 16 + rq + r;
+                if (row < mrows) a.c[static_cast<size_t>(m0 + row) * a.N + col] = res[t][r] + (acc[t][r] + bias);
+            }
+    } else if constexpr (EPI == kGemmQkv) {
+        // K/V columns: every row's cache slot and position requested before the first store, as
+        // above (a workgroup's 64 columns are all q or all K/V: 1280 is a multiple of 64).
+        const float bias = a.bias[col];
+        if (bx * kBN < kWidth) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = (t0 + 2 * t) * 16 + rq + r;
+                    if (row < mrows) a.c[static_cast<size_t>(m0 + row) * kWidth + col] = acc[t][r] + bias;
+                }
+        } else {
+            uint32_t rs[NT][4], rp[NT][4];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = (t0 + 2 * t) * 16 + rq + r, rc = m0 + (row < mrows ? row : 0);
+                    rs[t][r] = a.row_slot[rc];
+                    rp[t][r] = a.row_pos[rc];
+                }
+            const int rr = col - kWidth;
+            const bool is_v = rr >= kWidth;
+            const int c = is_v ? rr - kWidth : rr;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = (t0 + 2 * t) * 16 + rq + r;
+                    if (row < mrows) {
+                        const size_t off = static_cast<size_t>(rs[t][r]) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
+                                           (static_cast<size_t>(c >> 6) * a.kv_cap + rp[t][r]) * kHeadDim + (c & 63);
+                        a.kv[off] = acc[t][r] + bias;
+                    }
+                }
+        }
     } else {
         const float bias = a.bias[col];
 #pragma unroll
@@ -271,9 +329,24 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a) {
         return;
     }
     for (size_t e = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += static_cast<size_t>(gridDim.x) * blockDim.x) {
-        const float d = split_sum(a, e, plane);
         const int row = static_cast<int>(e / a.N), col = static_cast<int>(e % a.N);
-        gemm_store<EPI>(a, row, col, d + a.bias[col]);
+        const float bias = a.bias[col];
+        if constexpr (EPI == kGemmQkv) {
+            // the row's cache slot and position requested with the partials, not after them
+            const uint32_t rs = a.row_slot[row], rp = a.row_pos[row];
+            const float v = split_sum(a, e, plane) + bias;
+            if (col < kWidth) {
+                a.c[static_cast<size_t>(row) * kWidth + col] = v;
+            } else {
+                const int rr = col - kWidth;
+                const bool is_v = rr >= kWidth;
+                const int c = is_v ? rr - kWidth : rr;
+                a.kv[static_cast<size_t>(rs) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
+                     (static_cast<size_t>(c >> 6) * a.kv_cap + rp) * kHeadDim + (c & 63)] = v;
+            }
+        } else {
+            gemm_store<EPI>(a, row, col, split_sum(a, e, plane) + bias);
+        }
     }
 }
 
@@ -285,14 +358,40 @@ __global__ __launch_bounds__(256) void gemm_reduce_ln_kernel(GemmArgs a) {
     __shared__ float red[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const size_t plane = static_cast<size_t>(a.M) * a.N;
+    // Every load of the five columns before the first add and store, within one split-count
+    // case: per column, the split sums behind a branch and the store to c before the next
+    // column's loads made each column a memory round trip of its own.
     float v[1][5];
+    auto body = [&](auto sm) {
+        constexpr int SM = decltype(sm)::value;
+        float cv[5], bv[5], w[5][SM];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const int col = tid + 256 * i;
-        const size_t e = static_cast<size_t>(row) * a.N + col;
-        v[0][i] = a.c[e] + (split_sum(a, e, plane) + a.bias[col]);
-        a.c[e] = v[0][i];
-    }
+        for (int i = 0; i < 5; ++i) {
+            const int col = tid + 256 * i;
+            const size_t e = static_cast<size_t>(row) * a.N + col;
+            cv[i] = a.c[e];
+            bv[i] = a.bias[col];
+#pragma unroll
+            for (int z = 0; z < SM; ++z) w[i][z] = a.ws[static_cast<size_t>(min(z, a.splits - 1)) * plane + e];
+        }
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            float s = w[i][0];  // split_sum_n's order
+#pragma unroll
+            for (int z = 1; z < SM; ++z)
+                if (z < a.splits) s += w[i][z];
+            v[0][i] = cv[i] + (s + bv[i]);
+            a.c[static_cast<size_t>(row) * a.N + tid + 256 * i] = v[0][i];
+        }
+    };
+    if (a.splits <= 2)
+        body(std::integral_constant<int, 2>{});
+    else if (a.splits <= 4)
+        body(std::integral_constant<int, 4>{});
+    else if (a.splits <= 8)
+        body(std::integral_constant<int, 8>{});
+    else
+        body(std::integral_constant<int, kGemmMaxSplits>{});
     ln_block<1, 5>(v, a.ln_w, a.ln_b, red);
 #pragma unroll
     for (int i = 0; i < 5; ++i) a.ln_out[static_cast<size_t>(row) * kWidth + tid + 256 * i] = v[0][i];

@@ -26,6 +26,7 @@
 //   * codec_upsample: nearest x2 in time into the zero-padded input of the last conv.
 // A decode of a given length is captured once as a HIP graph and replayed (about 60 launches,
 // which bound short decodes); the padding rows are written by kernels, not memsets.
+#include <type_traits>
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -191,10 +192,28 @@ __global__ __launch_bounds__(256) void codec_reduce_kernel(CodecGemm g, int spli
     const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x, total = static_cast<size_t>(g.M) * g.N;
     if (i >= total) return;
     const int row = static_cast<int>(i / g.N), col = static_cast<int>(i % g.N);
-    float s = 0.0f;
-    for (int z = 0; z < splits; ++z) s += g.ws[z * total + i];
     float* p = g.c + static_cast<size_t>(row) * g.ldc + col;
-    *p = codec_epilogue(EPI, s + g.bias[col], EPI == kEpiScaleResid ? g.gamma[col] : 0.0f, p);
+    const float bias = g.bias[col], gamma = EPI == kEpiScaleResid ? g.gamma[col] : 0.0f;
+    const float res = EPI == kEpiScaleResid ? *p : 0.0f;
+    // every split's partial requested before the first add (SM >= splits; indices past the split
+    // count reread the last split and are not added): a loop of dependent adds over loads issued
+    // one at a time made each split a memory round trip
+    auto sum = [&](auto sm) {
+        constexpr int SM = decltype(sm)::value;
+        float w[SM];
+#pragma unroll
+        for (int z = 0; z < SM; ++z) w[z] = g.ws[static_cast<size_t>(min(z, splits - 1)) * total + i];
+        float s = 0.0f;
+#pragma unroll
+        for (int z = 0; z < SM; ++z)
+            if (z < splits) s += w[z];
+        return s;
+    };
+    const float s = splits <= 4 ? sum(std::integral_constant<int, 4>{})
+                    : splits <= 8 ? sum(std::integral_constant<int, 8>{})
+                    : splits <= 16 ? sum(std::integral_constant<int, 16>{})
+                                   : sum(std::integral_constant<int, 32>{});
+    *p = codec_epilogue(EPI, s + bias, gamma, &res);
 }
 
 // LayerNorm of a 384-wide row held as 6 values per lane (columns lane + 64 i): mean, then

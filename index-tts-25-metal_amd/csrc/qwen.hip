@@ -29,6 +29,7 @@
 // Prefill (P ids): embedding rows, RMSNorm rows, FP32 MFMA GEMMs of prefill.hip (store, residual
 // and SwiGLU epilogues, split K when tiles are few), q_prep_kernel over P rows, causal
 // attention, then the head on the last row.
+#include <type_traits>
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -480,15 +481,39 @@ __global__ __launch_bounds__(128) void q_attn_merge_kernel(QAttnArgs a) {
     if (!a.st->active) return;
     const int qh = blockIdx.x, d = threadIdx.x;
     const int splits = (static_cast<int>(a.st->cached) + 1 + kSplitRows - 1) / kSplitRows;
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, a.part_ml[(s * kQH + qh) * 2]);
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-        const float w = expf(a.part_ml[(s * kQH + qh) * 2] - M);
-        num = __builtin_fmaf(w, a.part_acc[(static_cast<size_t>(s) * kQH + qh) * kHd + d], num);
-        den = __builtin_fmaf(w, a.part_ml[(s * kQH + qh) * 2 + 1], den);
-    }
-    a.att[qh * kHd + d] = num / den;
+    // Every split's partials requested before the first use (SM >= splits; indices past the count
+    // reread the last split and are skipped): the loops over the splits issued one load at a
+    // time, each a memory round trip.  Same operations in the same order as before.
+    auto merge = [&](auto sm) {
+        constexpr int SM = decltype(sm)::value;
+        float m[SM], l[SM], v[SM];
+#pragma unroll
+        for (int s = 0; s < SM; ++s) {
+            const int sc = min(s, splits - 1);
+            m[s] = a.part_ml[(sc * kQH + qh) * 2];
+            l[s] = a.part_ml[(sc * kQH + qh) * 2 + 1];
+            v[s] = a.part_acc[(static_cast<size_t>(sc) * kQH + qh) * kHd + d];
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < SM; ++s)
+            if (s < splits) M = fmaxf(M, m[s]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SM; ++s)
+            if (s < splits) {
+                const float w = expf(m[s] - M);
+                num = __builtin_fmaf(w, v[s], num);
+                den = __builtin_fmaf(w, l[s], den);
+            }
+        a.att[qh * kHd + d] = num / den;
+    };
+    if (splits <= 8)
+        merge(std::integral_constant<int, 8>{});
+    else if (splits <= 32)
+        merge(std::integral_constant<int, 32>{});
+    else
+        merge(std::integral_constant<int, kMaxSplits>{});
 }
 
 // ------------------------------------------------------------------------ prefill pieces

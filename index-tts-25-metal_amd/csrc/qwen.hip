@@ -290,11 +290,16 @@ __global__ __launch_bounds__(1024) void q_argmax_kernel(QArgmaxArgs a) {
     const int t = threadIdx.x;
     float bv = -INFINITY;
     uint32_t bi = 0;
-    for (int k = t; k < a.nbest; k += 1024) {
-        const float2 b = a.best[k];
-        const uint32_t i = __float_as_uint(b.y);
-        if (better(b.x, i, bv, bi)) {
-            bv = b.x;
+    // every best this thread folds requested at once (kHeadBlocks bounds nbest), in the same order
+    constexpr int KB = (kHeadBlocks + 1023) / 1024;
+    float2 bs[KB];
+#pragma unroll
+    for (int r = 0; r < KB; ++r) bs[r] = a.best[min(t + 1024 * r, a.nbest - 1)];
+#pragma unroll
+    for (int r = 0; r < KB; ++r) {
+        const uint32_t i = __float_as_uint(bs[r].y);
+        if (t + 1024 * r < a.nbest && better(bs[r].x, i, bv, bi)) {
+            bv = bs[r].x;
             bi = i;
         }
     }

@@ -172,15 +172,40 @@ __global__ __launch_bounds__(256) void codec_gemm_kernel(CodecGemm g) {
     }
     // D layout of v_mfma_f32_32x32x2f32: lane l, element i -> row 8(i/4) + 4(l/32) + i%4, col l%32.
     const int col = n0 + wn * 32 + (lane & 31);
+    auto row_of = [&](int i) { return m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); };
+    if constexpr (PARTIAL) {
+        // Every destination formed before the first store: with one register pair reused for
+        // each row's address, the compiler waited for each store to complete before forming
+        // the next address.
+        float* dst[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int row = m0 + wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row >= g.M) continue;
-        if constexpr (PARTIAL) {
-            g.ws[(static_cast<size_t>(blockIdx.z) * g.M + row) * g.N + col] = acc[i];
-        } else {
-            float* p = g.c + static_cast<size_t>(row) * g.ldc + col;
-            *p = codec_epilogue(EPI, acc[i] + g.bias[col], EPI == kEpiScaleResid ? g.gamma[col] : 0.0f, p);
+        for (int i = 0; i < 16; ++i) {
+            dst[i] = g.ws + (static_cast<size_t>(blockIdx.z) * g.M + row_of(i)) * g.N + col;
+            asm volatile("" ::"v"(dst[i]));
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (row_of(i) < g.M) *dst[i] = acc[i];
+    } else {
+        // Bias and gamma read once, every row's residual requested before the first store (rows
+        // past M reread row M - 1, in bounds, and store nothing), and every value formed before
+        // the first store.  Read per element behind the stores into C, which may alias them,
+        // each was a memory round trip; and a use of a load inside a row's branch made the
+        // compiler wait there for every access in flight, the earlier rows' stores included.
+        const float bias = g.bias[col], gamma = EPI == kEpiScaleResid ? g.gamma[col] : 0.0f;
+        float res[16], out[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            res[i] = EPI == kEpiScaleResid ? g.c[static_cast<size_t>(min(row_of(i), g.M - 1)) * g.ldc + col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            out[i] = codec_epilogue(EPI, acc[i] + bias, gamma, &res[i]);
+            asm volatile("" ::"v"(out[i]));  // formed here, not sunk into the row's branch
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = row_of(i);
+            if (row < g.M) g.c[static_cast<size_t>(row) * g.ldc + col] = out[i];
         }
     }
 }

@@ -75,6 +75,16 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, int row, int col, 
     }
 }
 
+// A value held in a register at this point of the program: an empty asm takes it.  The GEMM
+// epilogues form every output (and read every loaded operand) before the first row's store
+// this way; left to the compiler, each row's arithmetic sank into that row's branch, where the
+// use of a load still in flight made it wait for every memory access outstanding, the
+// earlier rows' stores included (one store completion per row).
+template <typename T>
+__device__ __forceinline__ void pin_value(T v) {
+    asm volatile("" ::"v"(v));
+}
+
 // SiLU-gated product of one (gate, up) column pair (kernels.metal:363-374).
 __device__ __forceinline__ float swiglu_f(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
@@ -214,6 +224,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
     } else if constexpr (EPI == kGemmSwiglu) {
         // columns col and col ^ 1 sit in lanes l and l ^ 1, on the same rows
         const float bias = a.bias[col];
+        float out[NT][4];
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -221,7 +232,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
                 const int row = (t0 + 2 * t) * 16 + rq + r;
                 const float v = acc[t][r] + bias;
                 const float u = __shfl_xor(v, 1, 64);
-                if (row < mrows && !(col & 1)) a.c[static_cast<size_t>(m0 + row) * (a.N / 2) + col / 2] = swiglu_f(v, u);
+                out[t][r] = swiglu_f(v, u);
+                pin_value(out[t][r]);
+            }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = (t0 + 2 * t) * 16 + rq + r;
+                if (row < mrows && !(col & 1)) a.c[static_cast<size_t>(m0 + row) * (a.N / 2) + col / 2] = out[t][r];
             }
     } else if constexpr (EPI == kGemmResid) {
         // Every row's residual requested before the first store (rows past the block read the
@@ -235,24 +254,40 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
                 const int row = (t0 + 2 * t) * 16 + rq + r;
                 res[t][r] = a.c[static_cast<size_t>(m0 + (row < mrows ? row : 0)) * a.N + col];
             }
+        float out[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                out[t][r] = res[t][r] + (acc[t][r] + bias);
+                pin_value(out[t][r]);
+            }
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = (t0 + 2 * t) * 16 + rq + r;
-                if (row < mrows) a.c[static_cast<size_t>(m0 + row) * a.N + col] = res[t][r] + (acc[t][r] + bias);
+                if (row < mrows) a.c[static_cast<size_t>(m0 + row) * a.N + col] = out[t][r];
             }
     } else if constexpr (EPI == kGemmQkv) {
         // K/V columns: every row's cache slot and position requested before the first store, as
         // above (a workgroup's 64 columns are all q or all K/V: 1280 is a multiple of 64).
         const float bias = a.bias[col];
+        float out[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                out[t][r] = acc[t][r] + bias;
+                pin_value(out[t][r]);
+            }
         if (bx * kBN < kWidth) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = (t0 + 2 * t) * 16 + rq + r;
-                    if (row < mrows) a.c[static_cast<size_t>(m0 + row) * kWidth + col] = acc[t][r] + bias;
+                    if (row < mrows) a.c[static_cast<size_t>(m0 + row) * kWidth + col] = out[t][r];
                 }
         } else {
             uint32_t rs[NT][4], rp[NT][4];
@@ -263,6 +298,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
                     const int row = (t0 + 2 * t) * 16 + rq + r, rc = m0 + (row < mrows ? row : 0);
                     rs[t][r] = a.row_slot[rc];
                     rp[t][r] = a.row_pos[rc];
+                }
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pin_value(rs[t][r]);
+                    pin_value(rp[t][r]);
                 }
             const int rr = col - kWidth;
             const bool is_v = rr >= kWidth;
@@ -275,18 +317,27 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
                     if (row < mrows) {
                         const size_t off = static_cast<size_t>(rs[t][r]) * a.kv_slot_stride + a.kv_layer_off + (is_v ? a.kv_v_off : 0) +
                                            (static_cast<size_t>(c >> 6) * a.kv_cap + rp[t][r]) * kHeadDim + (c & 63);
-                        a.kv[off] = acc[t][r] + bias;
+                        a.kv[off] = out[t][r];
                     }
                 }
         }
     } else {
+        // Every value (GELU included) formed before the first store, as above.
         const float bias = a.bias[col];
+        float out[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                out[t][r] = EPI == kGemmGelu ? gelu_f(acc[t][r] + bias) : acc[t][r] + bias;
+                pin_value(out[t][r]);
+            }
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = (t0 + 2 * t) * 16 + rq + r;
-                if (row < mrows) gemm_store<EPI>(a, m0 + row, col, acc[t][r] + bias);
+                if (row < mrows) a.c[static_cast<size_t>(m0 + row) * a.N + col] = out[t][r];
             }
     }
 }

@@ -483,21 +483,48 @@ __global__ __launch_bounds__(256) void q_attn_kernel(QAttnArgs a) {
 
 // The splits of each query head merged with exp(m_s - M) rescaling, in split order.
 __global__ __launch_bounds__(128) void q_attn_merge_kernel(QAttnArgs a) {
-    if (!a.st->active) return;
     const int qh = blockIdx.x, d = threadIdx.x;
-    const int splits = (static_cast<int>(a.st->cached) + 1 + kSplitRows - 1) / kSplitRows;
-    // Every split's partials requested before the first use (SM >= splits; indices past the count
-    // reread the last split and are skipped): the loops over the splits issued one load at a
-    // time, each a memory round trip.  Same operations in the same order as before.
+    // The flag and the row count, requested first and together (scalar loads: no asm statement
+    // precedes them, which the compiler would count as a possible store).  The empty asm below
+    // keeps both loads above it, so the count is not read behind a branch on the flag.
+    const uint32_t act = a.st->active, cached = a.st->cached;
+    // The first PE splits' partials are requested before the split count is known (a cache of
+    // up to 512 rows then waits for one memory round trip, not two); splits past the count are
+    // skipped below, whatever was read for them.  The (max, sum) pairs are read at a per-lane
+    // offset of zero that the compiler cannot see through: as uniform scalar loads they were
+    // spilled to vector lanes and waited for one at a time.
+    constexpr int PE = 8;
+    static_assert(PE <= kMaxSplits, "the partial buffers hold kMaxSplits splits");
+    int vz = 0;
+    asm volatile("" : "+v"(vz));
+    const float* ml = a.part_ml + vz;
+    float m0[PE], l0[PE], v0[PE];
+#pragma unroll
+    for (int s = 0; s < PE; ++s) {
+        m0[s] = ml[(s * kQH + qh) * 2];
+        l0[s] = ml[(s * kQH + qh) * 2 + 1];
+        v0[s] = a.part_acc[(static_cast<size_t>(s) * kQH + qh) * kHd + d];
+    }
+    const bool active = act != 0;
+    const int splits = active ? (static_cast<int>(cached) + 1 + kSplitRows - 1) / kSplitRows : 0;
+    // Every further split's partials requested before the first use (SM >= splits; indices past
+    // the count reread the last split and are skipped): the loops over the splits issued one
+    // load at a time, each a memory round trip.  Same operations in the same order as before.
     auto merge = [&](auto sm) {
         constexpr int SM = decltype(sm)::value;
         float m[SM], l[SM], v[SM];
 #pragma unroll
         for (int s = 0; s < SM; ++s) {
-            const int sc = min(s, splits - 1);
-            m[s] = a.part_ml[(sc * kQH + qh) * 2];
-            l[s] = a.part_ml[(sc * kQH + qh) * 2 + 1];
-            v[s] = a.part_acc[(static_cast<size_t>(sc) * kQH + qh) * kHd + d];
+            if (s < PE) {
+                m[s] = m0[s];
+                l[s] = l0[s];
+                v[s] = v0[s];
+            } else {
+                const int sc = min(s, splits - 1);
+                m[s] = ml[(sc * kQH + qh) * 2];
+                l[s] = ml[(sc * kQH + qh) * 2 + 1];
+                v[s] = a.part_acc[(static_cast<size_t>(sc) * kQH + qh) * kHd + d];
+            }
         }
         float M = -INFINITY;
 #pragma unroll
@@ -511,10 +538,10 @@ __global__ __launch_bounds__(128) void q_attn_merge_kernel(QAttnArgs a) {
                 num = __builtin_fmaf(w, v[s], num);
                 den = __builtin_fmaf(w, l[s], den);
             }
-        a.att[qh * kHd + d] = num / den;
+        if (active) a.att[qh * kHd + d] = num / den;
     };
-    if (splits <= 8)
-        merge(std::integral_constant<int, 8>{});
+    if (splits <= PE)
+        merge(std::integral_constant<int, PE>{});
     else if (splits <= 32)
         merge(std::integral_constant<int, 32>{});
     else

@@ -158,10 +158,20 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     const float ebias = a.bias[erow];
     float eresid = 0.0f;
     if constexpr (EPI == kEpiResid) eresid = a.resid[eb * a.out_stride + erow];
-    // Whether any sequence is still decoding, read only now that the weights are requested:
-    // a live step's weight loads then never wait for this round trip.  A replay after every
-    // sequence finished still streams the weights once, but stores nothing.
-    {
+    // Whether any sequence is still decoding.  A replay after every sequence finished still
+    // streams the weights once, but stores nothing.
+    //   * 8 or more sequences: one vector load (lane b < B reads sequence b's flag) whose answer
+    //     is needed only before the stores, when every load has landed.  Read as scalar loads
+    //     behind the b < nseq tests, each flag was a round trip of its own, and the eight or
+    //     ten of them outlasted the weight stream (batch 8: 6720 -> 6802 decode tokens/s).
+    //   * fewer: those scalar loads, read only now that the weights are requested, return within
+    //     the weight stream; the vote measured slower there (3 beams: 3415 -> 3368 tokens/s).
+    constexpr bool kVote = B >= 8;
+    const bool fl_live = kVote && lane < B && lane < a.nseq;
+    uint32_t fl = 0;
+    if constexpr (kVote) {
+        fl = a.state[fl_live ? lane : 0].active;
+    } else {
         uint32_t any = 0;
 #pragma unroll
         for (int b = 0; b < B; ++b)
@@ -296,6 +306,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     float sum = red4[0];
 #pragma unroll
     for (int k = 1; k < NK; ++k) sum = lw == k ? red4[k] : sum;
+    if (kVote && !__any(fl_live && fl != 0)) return;  // every lane of the wave votes, before any leaves
     if (lw >= NK || i >= NV) return;
     const int b = eb;
     const int row = row0 + er;

@@ -213,13 +213,24 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a, int kchu
     const int col = bx * kBN + strip * 16 + (lane & 15);
     const int rq = 4 * (lane >> 4);
     if constexpr (SPLIT) {
+        // Every destination's 32-bit element offset formed before the first store (a split's
+        // plane is M x N < 2^31 elements): with one register pair reused for each row's
+        // address, the compiler let only about two stores be in flight at a time.
         float* ws = a.ws + static_cast<size_t>(bz) * a.M * a.N;
+        uint32_t off[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                off[t][r] = static_cast<uint32_t>((m0 + (t0 + 2 * t) * 16 + rq + r) * a.N + col);
+                pin_value(off[t][r]);
+            }
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = (t0 + 2 * t) * 16 + rq + r;
-                if (row < mrows) ws[static_cast<size_t>(m0 + row) * a.N + col] = acc[t][r];
+                if (row < mrows) ws[off[t][r]] = acc[t][r];
             }
     } else if constexpr (EPI == kGemmSwiglu) {
         // columns col and col ^ 1 sit in lanes l and l ^ 1, on the same rows

@@ -642,38 +642,69 @@ __device__ inline uint32_t draw_tokens_lds(SmemT<NTT>& sm, uint32_t m, const dou
 // step kernel): the processors and the draw on row b of the logits, then, in decode mode, the
 // token accepted and the state advanced (gpt_sampling.cpp:168-189 per step).  Every thread of
 // the workgroup calls it.
-template <int NTT, bool SEEN_AT_ONCE = false>
-__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b);
+// STANDALONE: the sampler kernel's own launch.  Its loads are ordered for a kernel that runs by
+// itself: the repetition set's bytes are requested at once (run_processors' SEEN_AT_ONCE), the
+// logits before the state's active flag is tested, and the state entry is read once into
+// registers (st below).  The step kernel's fused tail keeps the plain form, which its own
+// schedule was measured with: there, the same source changes made the whole step 12% slower.
+template <int NTT, bool STANDALONE = false>
+__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b, const SeqState& st);
+template <int NTT, bool STANDALONE = false>
+__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b) {
+    sample_loaded<NTT, STANDALONE>(sm, a, b, a.state[b]);
+}
 
-template <int NTT, bool SEEN_AT_ONCE = false>
+template <int NTT, bool STANDALONE = false>
 __device__ inline void sample_sequence(SmemT<NTT>& sm, const SampleArgs& a, int b) {
     [[maybe_unused]] constexpr int NT = NTT, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x;
-    const SeqState& st = a.state[b];
-    if (a.mode == kModeDecode && !st.active) return;
     const float* lg = a.logits + static_cast<size_t>(b) * a.logit_stride;
-    float v[IPT];  // all loads in flight before the first store
+    if constexpr (STANDALONE) {
+        // The logits requested first, then the whole state entry (one request, so no later field
+        // read waits behind a store that might alias it); the flag tested only then.  Testing it
+        // first made the logits wait for its round trip.
+        float v[IPT];
 #pragma unroll
-    for (int q = 0; q < IPT; ++q) {
-        const int i = t + q * NT;
-        v[q] = i < V ? lg[i] : 0.0f;
-    }
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            v[q] = i < V ? lg[i] : 0.0f;
+        }
+        const SeqState st = a.state[b];
+        if (a.mode == kModeDecode && !st.active) return;
 #pragma unroll
-    for (int q = 0; q < IPT; ++q) {
-        const int i = t + q * NT;
-        if (i < V) sm.s[i] = v[q];
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V) sm.s[i] = v[q];
+        }
+        __syncthreads();
+        sample_loaded<NTT, true>(sm, a, b, st);
+    } else {
+        const SeqState& st = a.state[b];
+        if (a.mode == kModeDecode && !st.active) return;
+        float v[IPT];  // all loads in flight before the first store
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            v[q] = i < V ? lg[i] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < IPT; ++q) {
+            const int i = t + q * NT;
+            if (i < V) sm.s[i] = v[q];
+        }
+        __syncthreads();
+        sample_loaded<NTT, false>(sm, a, b);
     }
-    __syncthreads();
-    sample_loaded<NTT, SEEN_AT_ONCE>(sm, a, b);
 }
 
 // sample_sequence after the scores are in sm.s (every thread calls it; decode mode expects an
-// active state).
-template <int NTT, bool SEEN_AT_ONCE>
-__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b) {
+// active state).  st: the state entry as read (the entry itself, or the standalone sampler's
+// copy in registers); every write goes to the entry, sw.
+template <int NTT, bool STANDALONE>
+__device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b, const SeqState& st) {
     [[maybe_unused]] constexpr int NT = NTT, IPT = (V + NTT - 1) / NTT;
     const int t = threadIdx.x;
-    SeqState& st = a.state[b];
+    SeqState& sw = a.state[b];
     const bool processors = a.mode != kModeDraw;
     const bool need_sample = a.mode == kModeDraw || (a.mode == kModeDecode && st.do_sample);
     if (processors && st.suppress_stop) {  // raw logits 8192 and 8193 dropped before any processor
@@ -687,7 +718,7 @@ __device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b)
     uint32_t status = kOk;
     bool topp = false;
     if (processors)
-        status = run_processors<NTT, SEEN_AT_ONCE>(sm, a.seen + static_cast<size_t>(b) * V, st.penalty, st.temperature, st.top_k, st.top_p,
+        status = run_processors<NTT, STANDALONE>(sm, a.seen + static_cast<size_t>(b) * V, st.penalty, st.temperature, st.top_k, st.top_p,
                                 st.num_beams, Pg, a.mode == kModeProcessors, &topp);
     uint32_t token = 0;
     if (status == kOk) {
@@ -724,36 +755,68 @@ __device__ inline void sample_loaded(SmemT<NTT>& sm, const SampleArgs& a, int b)
                         if (a.mode == kModeDraw && t == 0) a.out_tokens[d] = token;
                     }
                 }
-                if (t == 0) st.rng = rng;
+                if (t == 0) sw.rng = rng;
             }
         }
     }
     if (t != 0) return;
+    if constexpr (STANDALONE) {
+        // Accept the token and advance the state (gpt_sampling.cpp:181-186), from the fields
+        // read at the start: read after the stores below, each waited for the store before it.
+        a.status[b] = status;
+        if (a.mode != kModeDecode) return;
+        if (status != kOk) {
+            sw.error = 1;
+            sw.active = 0;
+            return;
+        }
+        if (token == static_cast<uint32_t>(kMelStop)) {
+            sw.stopped = 1;
+            sw.active = 0;
+        } else if (token >= static_cast<uint32_t>(kMelStart)) {
+            a.status[b] = kInvalidCode;
+            sw.error = 1;
+            sw.active = 0;
+        } else {
+            const uint32_t count = st.count + 1;
+            a.codes[static_cast<size_t>(b) * a.code_stride + st.count] = token;
+            sw.count = count;
+            a.seen[static_cast<size_t>(b) * V + token] = 1;
+            if (count >= st.max_tokens) {
+                sw.active = 0;
+            } else {
+                sw.token = token;
+                sw.position = count + 1;  // the first generated code sits at mel position 2
+                sw.n = st.prefix_rows + count - 1;
+            }
+        }
+        return;
+    }
     a.status[b] = status;
     if (a.mode != kModeDecode) return;
     if (status != kOk) {
-        st.error = 1;
-        st.active = 0;
+        sw.error = 1;
+        sw.active = 0;
         return;
     }
     // Accept the token and advance the state (gpt_sampling.cpp:181-186).
     if (token == static_cast<uint32_t>(kMelStop)) {
-        st.stopped = 1;
-        st.active = 0;
+        sw.stopped = 1;
+        sw.active = 0;
     } else if (token >= static_cast<uint32_t>(kMelStart)) {
         a.status[b] = kInvalidCode;
-        st.error = 1;
-        st.active = 0;
+        sw.error = 1;
+        sw.active = 0;
     } else {
-        a.codes[static_cast<size_t>(b) * a.code_stride + st.count] = token;
-        st.count += 1;
+        a.codes[static_cast<size_t>(b) * a.code_stride + sw.count] = token;
+        sw.count += 1;
         a.seen[static_cast<size_t>(b) * V + token] = 1;
-        if (st.count >= st.max_tokens) {
-            st.active = 0;
+        if (sw.count >= sw.max_tokens) {
+            sw.active = 0;
         } else {
-            st.token = token;
-            st.position = st.count + 1;  // the first generated code sits at mel position 2
-            st.n = st.prefix_rows + st.count - 1;
+            sw.token = token;
+            sw.position = sw.count + 1;  // the first generated code sits at mel position 2
+            sw.n = sw.prefix_rows + sw.count - 1;
         }
     }
 }

@@ -545,30 +545,15 @@ __device__ __forceinline__ void copy_block(uint8_t* __restrict__ dst, const uint
 // whole workgroup: the first `beams` repetition sets and table rows (each a contiguous block)
 // are staged, then each child's written from its parent's.  A repetition set (8194 bytes,
 // rows 2-byte aligned) is copied in 2-byte pieces, the child's token set in its piece.
-// The candidates go to LDS, and the parent count and the state template to thread 0's
-// registers, all requested with the staging copies: thread 0 read the candidates one at a
-// time (its loop can stop early) and the template once per child (behind the previous child's
-// state store, which might alias it), each a memory round trip with the rest of wave 0 waiting.
 __global__ __launch_bounds__(NT) void beam_advance_kernel(BeamAdvanceArgs a) {
     __shared__ uint32_t par_s[kMaxBatch], tok_s[kMaxBatch];
-    __shared__ BeamCand cand_s[kMaxBeamTake];
     const int t = threadIdx.x;
     const int beams = a.beams;
-    if (t < a.take) cand_s[t] = a.cand[t];
-    uint32_t P = 0;
-    SeqState tmpl{};
     if (t == 0) {
-        P = *a.parents_dev;
-        tmpl = *a.tmpl;
-    }
-    const uint32_t n = a.n, cap = a.cap;
-    copy_block(a.seen_tmp, a.seen, static_cast<uint32_t>(beams) * V);
-    copy_block(a.table_tmp, a.table, static_cast<uint32_t>(beams) * cap);
-    __syncthreads();  // cand_s
-    if (t == 0) {
+        const uint32_t P = *a.parents_dev;
         int C = 0;
         for (int r = 0; r < a.take && C < beams; ++r) {
-            const BeamCand c = cand_s[r];
+            const BeamCand c = a.cand[r];
             if (c.token == static_cast<uint32_t>(kMelStop)) continue;
             if (c.token >= static_cast<uint32_t>(kMelStart) || c.parent >= P) {
                 C = 0;
@@ -580,7 +565,7 @@ __global__ __launch_bounds__(NT) void beam_advance_kernel(BeamAdvanceArgs a) {
             ++C;
         }
         for (int c = 0; c < beams; ++c) {
-            SeqState st = tmpl;
+            SeqState st = *a.tmpl;
             st.n = a.n;
             st.position = a.position;
             if (c < C) {
@@ -598,6 +583,9 @@ __global__ __launch_bounds__(NT) void beam_advance_kernel(BeamAdvanceArgs a) {
         }
         *a.parents_dev = C > 0 ? static_cast<uint32_t>(C) : 1u;
     }
+    const uint32_t n = a.n, cap = a.cap;
+    copy_block(a.seen_tmp, a.seen, static_cast<uint32_t>(beams) * V);
+    copy_block(a.table_tmp, a.table, static_cast<uint32_t>(beams) * cap);
     __syncthreads();  // the staged rows, par_s and tok_s are seen by the whole workgroup
     static_assert(V % 2 == 0, "repetition sets in 2-byte pieces");
     constexpr uint32_t kHalf = V / 2;

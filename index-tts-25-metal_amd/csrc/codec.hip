@@ -177,15 +177,15 @@ __global__ __launch_bounds__(256) void codec_gemm_kernel(CodecGemm g) {
         // Every destination formed before the first store: with one register pair reused for
         // each row's address, the compiler waited for each store to complete before forming
         // the next address.
-        float* dst[16];
+        size_t dst[16];  // element offsets into ws (rows past M are formed, never stored to)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            dst[i] = g.ws + (static_cast<size_t>(blockIdx.z) * g.M + row_of(i)) * g.N + col;
+            dst[i] = (static_cast<size_t>(blockIdx.z) * g.M + row_of(i)) * g.N + col;
             asm volatile("" ::"v"(dst[i]));
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-            if (row_of(i) < g.M) *dst[i] = acc[i];
+            if (row_of(i) < g.M) g.ws[dst[i]] = acc[i];
     } else {
         // Bias and gamma read once, every row's residual requested before the first store (rows
         // past M reread row M - 1, in bounds, and store nothing), and every value formed before

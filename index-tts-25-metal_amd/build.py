@@ -41,7 +41,11 @@ SOURCES = ["decode.hip", "step.hip", "step_batch.hip", "sampler.hip", "beam.hip"
 # Per-file device flags.  step.hip: the persistent step kernel is scheduled with LLVM's max-ILP
 # strategy, 578.4 -> 567.9 us per step at 752 cached rows (one box, three alternating runs); the
 # same strategy made the batched GEMVs of decode.hip 9% slower, so it is not applied there.
-SOURCE_FLAGS = {"step.hip": ["-mllvm", "--amdgpu-sched-strategy=max-ilp"]}
+# codec.hip: the same strategy, 47-code decode 0.367 -> 0.356 ms, 600 codes 0.707 -> 0.705 ms
+# (one box, alternating).  Measured and not applied: max-ILP for prefill.hip (155-row prefill
+# 3.23 -> 3.29 ms) and qwen.hip (step 835 -> 846 us), no change for sampler.hip and beam.hip.
+_MAX_ILP = ["-mllvm", "--amdgpu-sched-strategy=max-ilp"]
+SOURCE_FLAGS = {"step.hip": _MAX_ILP, "codec.hip": _MAX_ILP}
 HOST_SOURCES = ["bundle.cpp"]  # host-only C++ (g++)
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"]
 

@@ -489,12 +489,62 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int b, int h, 
 }
 
 // Merge of the splits of one (sequence, head): out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-// Wave w takes splits w, w+4, ...; every load is issued before the first use.
+// The splits are taken as four chains, chain w holding splits w, w+4, ...; each chain's weighted
+// sums run in split order, then the four chains' sums are added in chain order.
+//   * at most 16 splits (caches up to 1024 rows): one wave runs all four chains, every load
+//     issued before the first use, with no LDS and no barrier;
+//   * more: wave w of four runs chain w, and the chains meet through LDS.
+// Both give the same operations in the same order, so the same bits.
+constexpr int kMergeOneWave = 16;
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a) {
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (b >= a.nseq || !a.state[b].active) return;
     const int S = live_splits(static_cast<int>(a.state[b].n) + 1, a.splits);
     const float* pb = a.partial + static_cast<size_t>(b * kHeads + h) * a.splits * 68;
+    if (S <= kMergeOneWave) {
+        if (wave != 0) return;  // waves 1-3 have nothing to do on this path
+        constexpr int PC = kMergeOneWave / 4;  // splits per chain
+        float mk[4][PC], lk[4][PC], ak[4][PC];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int i = 0; i < PC; ++i) {
+                const int k = w + 4 * i;
+                const bool ok = k < S;
+                mk[w][i] = ok ? pb[k * 68] : -INFINITY;
+                lk[w][i] = ok ? pb[k * 68 + 1] : 0.0f;
+                ak[w][i] = ok ? pb[k * 68 + 4 + lane] : 0.0f;
+            }
+        float wm[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < PC; ++i) m = fmaxf(m, mk[w][i]);
+            wm[w] = m;
+        }
+        const float mg = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+        float den[4], num[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            den[w] = 0.0f;
+            num[w] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PC; ++i) {
+                const float wgt = mk[w][i] == -INFINITY ? 0.0f : expf(mk[w][i] - mg);
+                den[w] = __builtin_fmaf(lk[w][i], wgt, den[w]);
+                num[w] = __builtin_fmaf(ak[w][i], wgt, num[w]);
+            }
+            // The four-wave form's chains always end with empty slots (each adds +0, which turns
+            // a -0 sum into +0): one such step here keeps even the sign of a zero the same.
+            den[w] = __builtin_fmaf(0.0f, 0.0f, den[w]);
+            num[w] = __builtin_fmaf(0.0f, 0.0f, num[w]);
+        }
+        const float d = ((den[0] + den[1]) + den[2]) + den[3];
+        const float n = ((num[0] + num[1]) + num[2]) + num[3];
+        a.out[b * kWidth + h * kHeadDim + lane] = n / d;
+        return;
+    }
     constexpr int PW = kAttnMaxSplits / 4;
     float mk[PW], lk[PW], ak[PW];
 #pragma unroll

@@ -40,28 +40,66 @@ __device__ __forceinline__ int live_splits(int L, int max_splits) { return attn_
 // registers.  The per-layer ln_1 and ln_2 are formed inside the batched GEMV instead
 // (kProStagedLn: from the staged rows in LDS, while the weights are in flight), which saves
 // this launch: 3.3 us per LayerNorm at 8 sequences.
+// One wave per sequence: lane l holds columns 64 w + l + 256 i (w < 4, i < 5), the values
+// ln_block<1, 5>'s thread 64 w + l holds, and ln_stats forms the statistics in that kernel's
+// order, so no barrier is needed.  Gamma and beta are requested with the row, before any store.
 template <int PRO>
-__global__ __launch_bounds__(256) void ln_seq_kernel(GemvArgs a) {
-    const int b = blockIdx.x, tid = threadIdx.x;
-    __shared__ float red[4];
-    float v[1][5];
+__global__ __launch_bounds__(64) void ln_seq_kernel(GemvArgs a) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    float v[4][5], g[4][5], be[4][5];
+    constexpr int NL = PRO == kProLn2 ? 2 : 1;
+    float g2[NL][4][5], be2[NL][4][5];
     if constexpr (PRO == kProEmbedLn) {
         const bool live = b < a.nseq;
         const uint32_t tok = live ? a.state[b].token : 0u, pos = live ? a.state[b].position : 0u;
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int c = tid + 256 * i;
-            v[0][i] = a.mel_emb[static_cast<size_t>(tok) * kWidth + c] + a.mel_pos[static_cast<size_t>(pos) * kWidth + c];
-            a.h_out[b * kWidth + c] = v[0][i];
-        }
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                const int c = 64 * w + lane + 256 * i;
+                v[w][i] = a.mel_emb[static_cast<size_t>(tok) * kWidth + c] + a.mel_pos[static_cast<size_t>(pos) * kWidth + c];
+            }
     } else {
 #pragma unroll
-        for (int i = 0; i < 5; ++i) v[0][i] = a.x[b * a.x_stride + tid + 256 * i];
-    }
-    ln_block<1, 5>(v, a.ln_w, a.ln_b, red);
-    if constexpr (PRO == kProLn2) ln_block<1, 5>(v, a.ln2_w, a.ln2_b, red);
+        for (int w = 0; w < 4; ++w)
 #pragma unroll
-    for (int i = 0; i < 5; ++i) a.xn[b * kWidth + tid + 256 * i] = v[0][i];
+            for (int i = 0; i < 5; ++i) v[w][i] = a.x[b * a.x_stride + 64 * w + lane + 256 * i];
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int c = 64 * w + lane + 256 * i;
+            g[w][i] = a.ln_w[c];
+            be[w][i] = a.ln_b[c];
+            if constexpr (PRO == kProLn2) {
+                g2[0][w][i] = a.ln2_w[c];
+                be2[0][w][i] = a.ln2_b[c];
+            }
+        }
+    if constexpr (PRO == kProEmbedLn) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int i = 0; i < 5; ++i) a.h_out[b * kWidth + 64 * w + lane + 256 * i] = v[w][i];
+    }
+    float mean, inv;
+    ln_stats(v, mean, inv);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int i = 0; i < 5; ++i) v[w][i] = ln_apply(v[w][i], mean, inv, g[w][i], be[w][i]);
+    if constexpr (PRO == kProLn2) {
+        ln_stats(v, mean, inv);
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int i = 0; i < 5; ++i) v[w][i] = ln_apply(v[w][i], mean, inv, g2[0][w][i], be2[0][w][i]);
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int i = 0; i < 5; ++i) a.xn[b * kWidth + 64 * w + lane + 256 * i] = v[w][i];
 }
 
 // NW waves per workgroup: 4 with a LayerNorm prologue or no input staging; a staged batched
@@ -593,7 +631,7 @@ int gemv_batch_bucket(int batch) {
 template <int PRO>
 hipError_t launch_ln_seq(const GemvArgs& a, int batch, hipStream_t s) {
     if (!a.xn) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((ln_seq_kernel<PRO>), dim3(gemv_batch_bucket(batch)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((ln_seq_kernel<PRO>), dim3(gemv_batch_bucket(batch)), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 GemvArgs staged_on_xn(const GemvArgs& a) {

@@ -151,7 +151,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     constexpr int XF = kWidth / 4;                  // 16-byte pieces per sequence and chunk
     constexpr int NX = WIDE ? B * PX : (B * XF + TPB - 1) / TPB;  // pieces per thread
     using XP = typename std::conditional<WIDE, float, float4>::type;
-    XP xr[STAGED ? NX : 1];
+    // Up to 4 sequences, 5120-wide rows are staged whole: every chunk's pieces requested up
+    // front and stored before one barrier, instead of a barrier per chunk (the LDS holds
+    // B x 5120 floats, 82 KB at 4).
+    constexpr bool FULL = STAGED && WIDE && B <= 4;
+    constexpr int NXR = FULL ? NCH * NX : NX;
+    XP xr[STAGED ? NXR : 1];
     auto x_piece = [&](int q, int i) -> XP {       // piece tid + TPB i of chunk q
         const int f = tid + TPB * i;
         if constexpr (WIDE) {  // i = b * PX + k: column tid + TPB k of sequence b
@@ -163,7 +168,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     };
     if constexpr (STAGED) {
 #pragma unroll
-        for (int i = 0; i < NX; ++i) xr[i] = x_piece(0, i);
+        for (int i = 0; i < NXR; ++i) xr[i] = x_piece(i / NX, i % NX);
     }
     // kProStagedLn: gamma and beta of the columns t + TPB k this thread normalises, also ahead
     // of the weights.
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
         if (!any) return;
     }
 
-    __shared__ float xs[PRO == kProNone ? 4 : (STAGED && COLS > kWidth ? 2 : 1) * B * kWidth];
+    __shared__ float xs[PRO == kProNone ? 4 : (FULL ? NCH : STAGED && COLS > kWidth ? 2 : 1) * B * kWidth];
     __shared__ float red[B * kNW];
     if constexpr (PRO != kProNone && !STAGED) {
         if constexpr (PRO == kProEmbedLn) {
@@ -246,21 +251,31 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
         // x through LDS, 1280 columns at a time (two buffers when there are several chunks):
         // chunk q + 1 is loaded into registers while chunk q's FMAs run.  Per (row, sequence)
         // the FMA chain runs over j in order, as below.
+        if constexpr (FULL) {
 #pragma unroll
-        for (int q = 0; q < NCH; ++q) {
-            float* xq = xs + (q & 1) * B * kWidth;
-#pragma unroll
-            for (int i = 0; i < NX; ++i) {
-                const int f = tid + TPB * i;
-                if (WIDE || f < B * XF) {
-                    if constexpr (WIDE) {
-                        xq[(i / PX) * kWidth + tid + TPB * (i % PX)] = xr[i];
-                    } else {
-                        *reinterpret_cast<float4*>(xq + (f / XF) * kWidth + (f % XF) * 4) = xr[i];
-                    }
-                }
+            for (int i = 0; i < NXR; ++i) {
+                const int q = i / NX, k = i % NX;
+                xs[q * B * kWidth + (k / PX) * kWidth + tid + TPB * (k % PX)] = xr[i];
             }
             __syncthreads();
+        }
+#pragma unroll
+        for (int q = 0; q < NCH; ++q) {
+            float* xq = xs + (FULL ? q : (q & 1)) * B * kWidth;
+            if constexpr (!FULL) {
+#pragma unroll
+                for (int i = 0; i < NX; ++i) {
+                    const int f = tid + TPB * i;
+                    if (WIDE || f < B * XF) {
+                        if constexpr (WIDE) {
+                            xq[(i / PX) * kWidth + tid + TPB * (i % PX)] = xr[i];
+                        } else {
+                            *reinterpret_cast<float4*>(xq + (f / XF) * kWidth + (f % XF) * 4) = xr[i];
+                        }
+                    }
+                }
+                __syncthreads();
+            }
             if constexpr (PRO == kProStagedLn) {
                 // Each sequence's mean and 1 / sqrt(var + eps) by one wave, in ln_block<1, 5>'s
                 // order (ln_stats), then every element normalised in place, as ln_block does:
@@ -286,7 +301,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
                     }
                 __syncthreads();
             }
-            if (q + 1 < NCH) {
+            if (!FULL && q + 1 < NCH) {
 #pragma unroll
                 for (int i = 0; i < NX; ++i) xr[i] = x_piece(q + 1, i);
             }

@@ -462,12 +462,12 @@ __global__ __launch_bounds__(256) void q_attn_kernel(QAttnArgs a) {
         gacc[g][1][j] = a1;
         __syncthreads();
         const int h = tid >> 7, d = tid & 127;
+        // Dimension d of group k's sum is float d of gacc[k][h] (component d & 3 of float4
+        // d >> 2), read as one float: a select over the four components compiled to a chain
+        // of branches, each waiting for its own LDS read.
         float s = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float4 v = gacc[k][h][d >> 2];
-            s += (d & 3) == 0 ? v.x : (d & 3) == 1 ? v.y : (d & 3) == 2 ? v.z : v.w;
-        }
+        for (int k = 0; k < 8; ++k) s += reinterpret_cast<const float*>(gacc[k][h])[d];
         const int qh = 2 * kvh + h;
         a.part_acc[(static_cast<size_t>(split) * kQH + qh) * kHd + d] = s;
         if (d == 0) {

@@ -157,15 +157,20 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f 
 
 // One head's per-head RMSNorm then RoPE at position pos (qwen.cpp:29-32; qwen_rope,
 // kernels.metal:3111-3115), by one wave: lane l holds dimensions l and l + 64, the pair the
-// rotation mixes.  Returns the two outputs.
-__device__ __forceinline__ float2 head_norm_rope(float x1, float x2, const float* g, const float* inv_freq, uint32_t pos) {
-    const int l = threadIdx.x & 63;
+// rotation mixes, with its weights g1 = g[l], g2 = g[l + 64] and frequency f = inv_freq[l].
+// Returns the two outputs.
+__device__ __forceinline__ float2 head_norm_rope(float x1, float x2, float g1, float g2, float f, uint32_t pos) {
     const float ss = wave_sum(__builtin_fmaf(x1, x1, x2 * x2));
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHd) + kEps);
-    const float n1 = x1 * inv * g[l], n2 = x2 * inv * g[l + 64];
+    const float n1 = x1 * inv * g1, n2 = x2 * inv * g2;
     float sn, cs;
-    sincosf(static_cast<float>(pos) * inv_freq[l], &sn, &cs);
+    sincosf(static_cast<float>(pos) * f, &sn, &cs);
     return make_float2(n1 * cs + (-n2) * sn, n2 * cs + n1 * sn);
+}
+// The same, reading the lane's weights from g and its frequency from inv_freq.
+__device__ __forceinline__ float2 head_norm_rope(float x1, float x2, const float* g, const float* inv_freq, uint32_t pos) {
+    const int l = threadIdx.x & 63;
+    return head_norm_rope(x1, x2, g[l], g[l + 64], inv_freq[l], pos);
 }
 
 // (v, i) replaces (bv, bi) under mit2_gpt_argmax_f32's rule (kernels.metal:1283-1297).
@@ -382,40 +387,55 @@ __global__ __launch_bounds__(256) void q_attn_kernel(QAttnArgs a) {
         const int split = t / kKVH, kvh = t % kKVH;
         float* kb = a.kc + static_cast<size_t>(kvh) * kCap * kHd;
         float* vb = a.vc + static_cast<size_t>(kvh) * kCap * kHd;
+        const int r0 = split * kSplitRows + g * 8;
+        // This wave's pair of projection values with its RMSNorm weights and RoPE frequency
+        // (waves 0, 1: the two query heads; 2: the step's K row; 3: its V row, used by the
+        // tile that holds the step's row), requested before the cache rows below so that the
+        // waits for them do not also wait for the rows (loads complete in order).
+        const int col = wave < 2 ? (2 * kvh + wave) * kHd : wave == 2 ? kQ + kvh * kHd : kQ + kKV + kvh * kHd;
+        const float* gw = wave < 2 ? a.q_norm : a.k_norm;
+        const float x1 = a.qkv[col + lane], x2 = a.qkv[col + lane + 64];
+        const float g1 = gw[lane], g2 = gw[lane + 64], fr = a.inv_freq[lane];
+        // The cached rows' K and V do not depend on this step's projection, so they are
+        // requested next and arrive while the query heads are formed.  Rows from `cached` on
+        // read row 0 (in bounds) and take the step's own row from LDS after the barrier.
+        float4 kr[8], vr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = r0 + i;
+            const size_t off = static_cast<size_t>(row < static_cast<int>(cached) ? row : 0) * kHd + 4 * j;
+            kr[i] = *reinterpret_cast<const float4*>(kb + off);
+            vr[i] = *reinterpret_cast<const float4*>(vb + off);
+        }
         if (wave < 2) {
-            const int col = (2 * kvh + wave) * kHd;
-            const float2 o = head_norm_rope(a.qkv[col + lane], a.qkv[col + lane + 64], a.q_norm, a.inv_freq, cached);
+            const float2 o = head_norm_rope(x1, x2, g1, g2, fr, cached);
             qs[wave][lane] = o.x;
             qs[wave][lane + 64] = o.y;
         } else if (split == own) {
             if (wave == 2) {
-                const int col = kQ + kvh * kHd;
-                const float2 o = head_norm_rope(a.qkv[col + lane], a.qkv[col + lane + 64], a.k_norm, a.inv_freq, cached);
+                const float2 o = head_norm_rope(x1, x2, g1, g2, fr, cached);
                 knew[lane] = o.x;
                 knew[lane + 64] = o.y;
                 kb[static_cast<size_t>(cached) * kHd + lane] = o.x;
                 kb[static_cast<size_t>(cached) * kHd + lane + 64] = o.y;
             } else {
-                const int col = kQ + kKV + kvh * kHd;
-                const float v1 = a.qkv[col + lane], v2 = a.qkv[col + lane + 64];
-                vnew[lane] = v1;
-                vnew[lane + 64] = v2;
-                vb[static_cast<size_t>(cached) * kHd + lane] = v1;
-                vb[static_cast<size_t>(cached) * kHd + lane + 64] = v2;
+                vnew[lane] = x1;
+                vnew[lane + 64] = x2;
+                vb[static_cast<size_t>(cached) * kHd + lane] = x1;
+                vb[static_cast<size_t>(cached) * kHd + lane + 64] = x2;
             }
         }
         __syncthreads();
-        const int r0 = split * kSplitRows + g * 8;
         const float4 q0 = *reinterpret_cast<const float4*>(&qs[0][4 * j]);
         const float4 q1 = *reinterpret_cast<const float4*>(&qs[1][4 * j]);
-        float4 kr[8], vr[8];
+        const float4 kn = *reinterpret_cast<const float4*>(&knew[4 * j]);
+        const float4 vn = *reinterpret_cast<const float4*>(&vnew[4 * j]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int row = r0 + i;
-            const bool cached_row = row < static_cast<int>(cached);
-            const size_t off = static_cast<size_t>(cached_row ? row : 0) * kHd + 4 * j;
-            kr[i] = cached_row ? *reinterpret_cast<const float4*>(kb + off) : *reinterpret_cast<const float4*>(&knew[4 * j]);
-            vr[i] = cached_row ? *reinterpret_cast<const float4*>(vb + off) : *reinterpret_cast<const float4*>(&vnew[4 * j]);
+            if (!(r0 + i < static_cast<int>(cached))) {
+                kr[i] = kn;
+                vr[i] = vn;
+            }
         }
         float s0[8], s1[8], m0 = -INFINITY, m1 = -INFINITY;
 #pragma unroll

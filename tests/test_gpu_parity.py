@@ -196,6 +196,50 @@ def test_sampled_generate_small(small, itts, oracle):
     assert r.codes == codes and r.stopped == stopped
 
 
+@pytest.mark.parametrize("opts", [
+    # no processor at all: plain softmax draws
+    dict(do_sample=True, seed=1, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0),
+    # top-k of one: every draw has a single survivor
+    dict(do_sample=True, seed=2, temperature=0.3, top_k=1, top_p=1.0, repetition_penalty=1.0),
+    # top-k at and past the vocabulary (gpt_sampling.cpp:58: no filter), top-p 0.5, mild penalty
+    dict(do_sample=True, seed=3, temperature=1.5, top_k=8194, top_p=0.5, repetition_penalty=2.0),
+    dict(do_sample=True, seed=4, temperature=1.0, top_k=10000, top_p=0.9, repetition_penalty=1.0),
+    # a tiny top-p (only the best survives) under the headline's other processors
+    dict(do_sample=True, seed=5, temperature=0.8, top_k=30, top_p=0.01, repetition_penalty=10.0),
+    # a penalty below one favours the codes in the history, the start code 8192 included
+    # (history {1, 8192}, gpt_sampling.cpp:174), so a draw of 8192 ends the call with the
+    # reference's "GPT generated invalid semantic code" (:180)
+    dict(do_sample=True, seed=6, temperature=1.0, top_k=5, top_p=0.99, repetition_penalty=0.7),
+    # greedy after the processors
+    dict(do_sample=False, temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=3.0),
+    # a seed above 2^63 and a high temperature
+    dict(do_sample=True, seed=2**63 + 5, temperature=2.0, top_k=100, top_p=0.95, repetition_penalty=1.2),
+    dict(do_sample=True, seed=0, temperature=0.05, top_k=50, top_p=0.8, repetition_penalty=10.0, suppress_stop=True),
+])
+def test_generate_option_sweep_matches_oracle(small, itts, oracle, opts):
+    """generate() on the device (processors, draw and SplitMix64 state, the history that the
+    repetition penalty reads, the stop rule, the invalid-code error) equals the oracle's
+    gpt_sampling.cpp:168-189 loop over option edge cases, at 2 layers: the same codes and stop
+    flag, or the same error message."""
+    dec, orc, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    o = itts.GenerationOptions(**opts)
+    print(f"option sweep {opts}", flush=True)
+    try:
+        r = dec.generate(prefix, o, 48)
+        got = ("codes", r.codes, r.stopped)
+    except itts.GptRuntimeError as e:
+        got = ("error", str(e))
+    try:
+        codes, stopped = orc.generate(prefix, oracle.options_from(o), 48)
+        want = ("codes", codes, stopped)
+    except oracle.OracleError as e:
+        want = ("error", str(e))
+    assert got == want
+    if got[0] == "codes":
+        assert dec.cached_tokens() == orc.cached_tokens()
+
+
 def test_batch_generate_matches_single_and_oracle(small, itts, oracle):
     dec, orc, cond, _ = small
     rng = np.random.default_rng(7)

@@ -256,6 +256,28 @@ def test_batch_generate_matches_single_and_oracle(small, itts, oracle):
         assert batch[b].codes == codes
 
 
+def test_batch_generate_mixed_options_match_oracle(small, itts, oracle):
+    """One batch whose sequences each carry different sampling options (greedy after the
+    processors, top-k 1, no processor at all, the stop code allowed) and ragged prefixes: each
+    sequence's codes and stop flag equal the oracle's single-sequence loop
+    (gpt_sampling.cpp:168-189) with its own options."""
+    dec, orc, cond, _ = small
+    rng = np.random.default_rng(11)
+    opts = [itts.GenerationOptions(do_sample=False, top_k=30, top_p=0.8, repetition_penalty=3.0),
+            itts.GenerationOptions(seed=21, temperature=0.3, top_k=1, top_p=1.0, repetition_penalty=1.0),
+            itts.GenerationOptions(seed=22, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0),
+            itts.GenerationOptions(seed=23, temperature=1.2, top_k=200, top_p=0.95, repetition_penalty=1.5)]
+    prefixes = []
+    for b in range(len(opts)):
+        t = rng.integers(0, 12000, int(rng.integers(5, 120))).astype(np.uint32)
+        prefixes.append(dec.prepare_cond(cond, t, 0))
+    print("mixed-option batch, prefix rows", [p.size // 1280 for p in prefixes], flush=True)
+    batch = dec.generate_batch(prefixes, opts, 40)
+    for b in range(len(opts)):
+        codes, stopped = orc.generate(prefixes[b], oracle.options_from(opts[b]), 40)
+        assert (batch[b].codes, batch[b].stopped) == (codes, stopped), b
+
+
 def _segment_case(itts, n, seed):
     rng = np.random.default_rng(seed)
     segments = [[int(x) for x in rng.integers(0, 12000, int(rng.integers(1, 40)))] for _ in range(n)]

@@ -92,6 +92,24 @@ def test_steps_past_1024_rows(pair):
     w.report()
 
 
+def test_steps_past_2048_rows(itts, oracle):
+    """One layer, a 2040-id prompt (32 attention splits) and 20 steps: the cache crosses row
+    2048, where the split merge takes its widest form (33 and more splits; the reference's
+    limits reach 3072 prompt ids + 1024 generated).  One layer keeps the oracle's prefill to
+    seconds."""
+    qw1 = itts.make_synthetic_qwen_weights(layers=1, seed=8)
+    dec = itts.QwenDecoder(qw1, layers=1)
+    orc = oracle.OracleQwen(qw1, layers=1)
+    w = Worst("qwen 1-layer, 2040-id prompt + 20 steps")
+    p = ids_of(6, 2060)
+    print("qwen prefill 2040 ids (1 layer)", flush=True)
+    w.check(dec.prefill(p[:2040]), orc.prefill(p[:2040]), "prefill")
+    for i in range(2040, 2060):
+        w.check(dec.step(p[i]), orc.step(p[i]), f"step at row {i}")
+    w.report()
+    dec.close()
+
+
 def test_greedy_generate_matches_oracle(pair):
     dec, orc = pair
     for n, maximum in ((12, 40), (130, 16), (5, 1)):

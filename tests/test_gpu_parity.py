@@ -431,6 +431,33 @@ def test_beam_search_matches_oracle(beam_small, itts, oracle, opts):
     assert dec.cached_tokens() == orc.cached_tokens()
 
 
+@pytest.mark.parametrize("opts", [
+    # a penalty below one favours every code in the history, the start code 8192 included
+    # (gpt_sampling.cpp:211), so a candidate 8192 ends the search with the reference's error (:233)
+    dict(do_sample=False, repetition_penalty=0.5, num_beams=3),
+    dict(do_sample=True, seed=12, num_beams=2, top_k=4, top_p=1.0, temperature=1.0, repetition_penalty=0.8),
+    # a tiny top-p: one survivor per parent beyond the two that beams keep (:62)
+    dict(do_sample=True, seed=13, num_beams=3, top_k=0, top_p=0.01, temperature=0.7, repetition_penalty=1.0),
+])
+def test_beam_search_edge_options_match_oracle(beam_small, itts, oracle, opts):
+    """Beam search over option edge cases: the device and the oracle (gpt_sampling.cpp:190-245)
+    give the same codes and stop flag, or the same error message."""
+    dec, orc, prefix = beam_small
+    o = itts.GenerationOptions(**opts)
+    print(f"beam edge options {opts}", flush=True)
+    try:
+        r = dec.generate(prefix, o, 24)
+        got = ("codes", r.codes, r.stopped)
+    except itts.GptRuntimeError as e:
+        got = ("error", str(e))
+    try:
+        codes, stopped = orc.generate(prefix, oracle.options_from(o), 24)
+        want = ("codes", codes, stopped)
+    except oracle.OracleError as e:
+        want = ("error", str(e))
+    assert got == want
+
+
 def test_beam_search_needs_capacity(beam_small, itts):
     dec, _, prefix = beam_small
     with pytest.raises(itts.InvalidArgument, match="max_batch"):

@@ -256,6 +256,26 @@ def test_batch_generate_matches_single_and_oracle(small, itts, oracle):
         assert batch[b].codes == codes
 
 
+@pytest.mark.parametrize("maximum", [1, 2, 3])
+def test_generate_shortest_runs_match_oracle(small, itts, oracle, maximum):
+    """generate() for 1-3 codes (gpt_sampling.cpp:176-185: no step after the last code), single
+    and batched, greedy and sampled, against the oracle; the cache then holds the prefix and
+    maximum - 1 steps."""
+    dec, orc, cond, text = small
+    prefix = dec.prepare_cond(cond, text, 0)
+    opts = [itts.GenerationOptions(do_sample=False, repetition_penalty=1.0, suppress_stop=True),
+            itts.GenerationOptions(seed=31, suppress_stop=True)]
+    for o in opts:
+        r = dec.generate(prefix, o, maximum)
+        codes, stopped = orc.generate(prefix, oracle.options_from(o), maximum)
+        assert (r.codes, r.stopped) == (codes, stopped) and len(codes) == maximum
+        assert dec.cached_tokens() == orc.cached_tokens() == prefix.size // 1280 + maximum - 1
+    batch = dec.generate_batch([prefix, prefix], opts, maximum)
+    for b, o in enumerate(opts):
+        codes, _ = orc.generate(prefix, oracle.options_from(o), maximum)
+        assert batch[b].codes == codes, b
+
+
 def test_batch_generate_mixed_options_match_oracle(small, itts, oracle):
     """One batch whose sequences each carry different sampling options (greedy after the
     processors, top-k 1, no processor at all, the stop code allowed) and ragged prefixes: each

@@ -276,6 +276,23 @@ def test_generate_shortest_runs_match_oracle(small, itts, oracle, maximum):
         assert batch[b].codes == codes, b
 
 
+def test_bf16_batch_equals_single(small_weights, itts):
+    """BF16-stored weights: a batch of ragged sequences gives each sequence the codes of its own
+    batch-1 generate(), bit for bit (the batched GEMVs keep batch 1's per-row FMA order and
+    reduction pairings)."""
+    d16 = itts.GptDecoder(small_weights, kv_capacity=1024, max_batch=4, weight_dtype="bf16")
+    cond, _ = itts.synthetic_prefix_inputs(30, seed=3)
+    rng = np.random.default_rng(17)
+    prefixes = [d16.prepare_cond(cond, rng.integers(0, 12000, int(rng.integers(5, 90))).astype(np.uint32), 0)
+                for _ in range(4)]
+    opts = [itts.GenerationOptions(seed=40 + b, suppress_stop=True) for b in range(4)]
+    batch = d16.generate_batch(prefixes, opts, 32)
+    for b in range(4):
+        single = d16.generate(prefixes[b], opts[b], 32)
+        assert (batch[b].codes, batch[b].stopped) == (single.codes, single.stopped), b
+    d16.close()
+
+
 def test_batch_generate_mixed_options_match_oracle(small, itts, oracle):
     """One batch whose sequences each carry different sampling options (greedy after the
     processors, top-k 1, no processor at all, the stop code allowed) and ragged prefixes: each
